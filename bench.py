@@ -1,0 +1,234 @@
+"""Benchmark of the MI355X continuous-batching attention path.
+
+One JSON line on stdout.  `value` is paged decode attention throughput in
+GB/s of algorithmic HBM traffic (K/V read once per kv head and context token,
+q read, out written, block tables and context lengths read), over a decode
+step of 32 sequences with context lengths uniform in [256, 2304] run through
+all 28 layers' KV caches of a Qwen3-0.6B-shaped model (16 q / 8 kv heads,
+head_dim 128, block_size 128, bf16): one "step" = 28 launches, one per layer,
+each reading its own layer's pages so the 256 MB Infinity Cache cannot serve
+them.  Inputs are resident in HBM before the timed region.
+
+Also reported: the roofline of the decode kernel (average launch duration from
+HIP events on the launch stream), the fp32 CPU oracle on the host cores as the
+CPU baseline, and (unless --no-e2e) the end-to-end output tok/s of the
+32 x 256-in / 2048-out greedy workload next to the reference's published
+910B3 figure.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+REFERENCE_E2E_TOK_S = 1296.05  # nano_vllm_ascend on Ascend 910B3, 32 x 256/2048, bench_outputs/nano_32x256_2048.json
+NUM_LAYERS = 28
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work budget of the baseline sample")
+    ap.add_argument("--e2e-prompts", type=int, default=32)
+    ap.add_argument("--e2e-input", type=int, default=256)
+    ap.add_argument("--e2e-output", type=int, default=2048)
+    return ap.parse_args()
+
+
+def load_traffic(workload: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters (committed under profiles/), if present."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+        entry = data.get(workload)
+        return None if entry is None else float(entry["bytes_per_launch"])
+    except Exception:
+        return None
+
+
+def decode_leg(args, device):
+    import torch
+
+    from nano_vllm_ascend_amd import _C
+    from nano_vllm_ascend_amd import workloads as W
+
+    work = W.decode_step(device, seed=args.seed, num_layers=NUM_LAYERS)
+    b = len(work.context_lens_list)
+    max_ctx = max(work.context_lens_list)
+    scale = W.HEAD_DIM ** -0.5
+    ws = _C.alloc_paged_decode_workspace(b, W.NUM_HEADS, W.NUM_KV_HEADS, max_ctx, device)
+    out = torch.empty_like(work.q)
+    bytes_per_launch = (
+        sum(work.context_lens_list) * W.NUM_KV_HEADS * W.HEAD_DIM * 2 * 2
+        + 2 * b * W.NUM_HEADS * W.HEAD_DIM * 2
+        + b * work.block_tables.shape[1] * 4
+        + b * 4
+    )
+    layers = [(work.key_cache[l], work.value_cache[l]) for l in range(NUM_LAYERS)]
+    stream = torch.cuda.current_stream()
+
+    def step(events=None):
+        for l, (kc, vc) in enumerate(layers):
+            _C.paged_decode(out, work.q, kc, vc, work.block_tables, work.context_lens, scale, max_ctx, ws)
+            if events is not None:
+                events.append(torch.cuda.Event(enable_timing=True))
+                events[-1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    events: list = []
+    start.record(stream)
+    for _ in range(args.steps):
+        step(events)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(events[-1])
+    marks = [start] + events
+    launch_ms = [marks[i].elapsed_time(marks[i + 1]) for i in range(len(events))]
+    avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
+    launches = args.steps * NUM_LAYERS
+    value = bytes_per_launch * launches / (total_ms / 1e3) / 1e9
+    achieved = bytes_per_launch / avg_launch_s / 1e9
+    return {
+        "value": value,
+        "ms_per_step": total_ms / args.steps,
+        "bytes_per_launch": bytes_per_launch,
+        "avg_launch_us": avg_launch_s * 1e6,
+        "achieved": achieved,
+        "work": work,
+        "max_ctx": max_ctx,
+    }
+
+
+def cpu_baseline(work, seconds: float):
+    """fp32 oracle on the host cores over a bounded sample: one layer's decode of the same batch, repeated."""
+    import torch
+
+    from oracle.attention_ref import paged_decode_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    b = len(work.context_lens_list)
+    bs = work.key_cache.shape[2]
+    # Copy only the pages the batch reads (layer 0), renumbered densely, to host memory.
+    bt = work.block_tables.cpu()
+    need = [(c + bs - 1) // bs for c in work.context_lens_list]
+    ids = torch.cat([bt[i, : need[i]] for i in range(b)]).long()
+    kc = work.key_cache[0][ids.to(work.key_cache.device)].cpu()
+    vc = work.value_cache[0][ids.to(work.value_cache.device)].cpu()
+    tables = torch.zeros_like(bt)
+    pos = 0
+    for i in range(b):
+        tables[i, : need[i]] = torch.arange(pos, pos + need[i], dtype=torch.int32)
+        pos += need[i]
+    q = work.q.cpu()
+    ctx = work.context_lens.cpu()
+    scale = 128 ** -0.5
+    paged_decode_ref(q, kc, vc, tables, ctx, scale)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        paged_decode_ref(q, kc, vc, tables, ctx, scale)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 200:
+            break
+    bytes_per = sum(work.context_lens_list) * 8 * 128 * 2 * 2 + 2 * b * 16 * 128 * 2 + b * bt.shape[1] * 4 + b * 4
+    return {
+        "value": bytes_per * reps / el / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"fp32 torch-CPU oracle, layer-0 decode of the same 32-sequence batch, {reps} reps in {el:.1f} s",
+        "cpu": platform.processor() or platform.machine(),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path shards by sequence or kv head with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+
+    dec = decode_leg(args, device)
+    workload = "decode_b32_ctx256-2304_28layers"
+    traffic = load_traffic(workload)
+    result = {
+        "metric": "paged decode-attn HBM GB/s (% of peak); Qwen3-0.6B output tok/s 32x256/2048",
+        "value": round(dec["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/K/V, seeded context lengths and block tables)",
+        "config": {
+            "workload": workload,
+            "batch": 32,
+            "context_lens": "uniform [256, 2304], seed %d" % args.seed,
+            "sum_context": sum(dec["work"].context_lens_list),
+            "layers_per_step": NUM_LAYERS,
+            "num_heads": 16,
+            "num_kv_heads": 8,
+            "head_dim": 128,
+            "block_size": 128,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode_kernel",
+            "achieved": round(dec["achieved"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec["achieved"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": dec["bytes_per_launch"],
+            "avg_launch_us": round(dec["avg_launch_us"], 3),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(dec["work"], args.cpu_seconds)
+    del dec
+    torch.cuda.empty_cache()
+    if not args.no_e2e:
+        try:
+            from nano_vllm_ascend_amd.bench_e2e import run_e2e
+        except ImportError:
+            run_e2e = None
+        if run_e2e is not None:
+            e2e = run_e2e(args.e2e_prompts, args.e2e_input, args.e2e_output, seed=args.seed, device=device)
+            e2e["vs_reference_910B3"] = round(e2e["output_tok_s"] / REFERENCE_E2E_TOK_S, 3)
+            result["e2e"] = e2e
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

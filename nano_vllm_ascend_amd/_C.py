@@ -1,0 +1,215 @@
+"""ctypes binding of ``libnvamd.so`` (the C ABI in ``include/nvamd.h``).
+
+The wrappers take torch tensors, check shapes the way the reference's Python
+layers do (ValueError on a shape mismatch), pass raw device pointers and the
+current HIP stream, and raise if the library reports an error.  There is no
+fallback: if the library is missing, every call raises, so a test or bench that
+passes has run the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libnvamd.so"
+
+NVAMD_OK = 0
+_ERRORS = {-1: "invalid argument", -2: "unsupported configuration", -3: "workspace missing or too small"}
+
+_c_int = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_c_ptr = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+_c_float = ctypes.c_float
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "nvamd_version": (_c_int, []),
+    "nvamd_paged_decode_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "nvamd_paged_decode": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_ptr,
+         _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_ptr, _c_size, _c_ptr],
+    ),
+    "nvamd_kv_cache_write": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_i64, _c_ptr],
+    ),
+    "nvamd_qk_norm_rope": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr,
+         _c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_float, _c_ptr],
+    ),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def exported_symbols() -> list[str]:
+    """Names the binding expects the library to export."""
+    return sorted(_SIGNATURES)
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once; raise RuntimeError if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m nano_vllm_ascend_amd.build` "
+            "(or __graft_entry__.build()); there is no CPU fallback"
+        )
+    lib = ctypes.CDLL(os.fspath(LIB_PATH))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def _check(status: int, name: str) -> None:
+    if status == NVAMD_OK:
+        return
+    if status < 0:
+        raise ValueError(f"{name}: {_ERRORS.get(status, 'error')} (status {status})")
+    raise RuntimeError(f"{name}: HIP launch failed with hipError_t {status}")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _row_stride(t: torch.Tensor) -> int:
+    """Element stride between tokens of a [T, heads, D] (or [T, heads*D]) view whose rows are dense."""
+    if t.dim() == 3:
+        _require(t.stride(2) == 1 and t.stride(1) == t.shape[2], f"rows of {tuple(t.shape)} are not dense")
+    else:
+        _require(t.stride(-1) == 1, f"rows of {tuple(t.shape)} are not dense")
+    return t.stride(0)
+
+
+def _bf16_cuda(name: str, t: torch.Tensor) -> None:
+    _require(t.dtype == torch.bfloat16, f"{name} must be bfloat16, got {t.dtype}")
+    _require(t.is_cuda, f"{name} must be on the GPU")
+
+
+def version() -> int:
+    return int(load().nvamd_version())
+
+
+def paged_decode_workspace_size(max_batch: int, num_heads: int, num_kv_heads: int, max_context_len: int) -> int:
+    return int(load().nvamd_paged_decode_workspace_size(max_batch, num_heads, num_kv_heads, max_context_len))
+
+
+def alloc_paged_decode_workspace(max_batch: int, num_heads: int, num_kv_heads: int, max_context_len: int,
+                                 device) -> torch.Tensor:
+    """Zero-filled workspace (the kernel keeps its counters at zero between calls)."""
+    nbytes = paged_decode_workspace_size(max_batch, num_heads, num_kv_heads, max_context_len)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
+def paged_decode(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                 block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float, max_context_len: int,
+                 workspace: torch.Tensor) -> torch.Tensor:
+    """out[i,h] = softmax(q[i,h] K^T * scale) V over the paged context of sequence i.
+
+    q/out: [B, Hq, 128] bf16 (dense rows, any token stride); caches
+    [NB, block_size, Hkv, 128] bf16; block_tables int32 [B, W]; context_lens
+    int32 [B] on the device; max_context_len bounds every context_lens entry.
+    """
+    lib = load()
+    _bf16_cuda("q", q)
+    _bf16_cuda("out", out)
+    _bf16_cuda("key_cache", key_cache)
+    _bf16_cuda("value_cache", value_cache)
+    _require(q.dim() == 3 and out.shape == q.shape, f"q/out shape mismatch: {tuple(q.shape)} vs {tuple(out.shape)}")
+    _require(key_cache.dim() == 4 and key_cache.shape == value_cache.shape, "key/value cache shape mismatch")
+    _require(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    nb, bs, hkv, d = key_cache.shape
+    b, hq, dq = q.shape
+    _require(dq == d, f"head_dim mismatch {dq} vs {d}")
+    _require(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and block_tables.shape[0] == b,
+             "block_tables must be int32 [B, W]")
+    _require(block_tables.stride(1) == 1, "block_tables rows must be dense")
+    _require(context_lens.dtype == torch.int32 and context_lens.numel() == b and context_lens.is_cuda,
+             "context_lens must be int32 [B] on the device")
+    _require(context_lens.is_contiguous(), "context_lens must be contiguous")
+    status = lib.nvamd_paged_decode(
+        out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), key_cache.data_ptr(),
+        value_cache.data_ptr(), nb, bs, block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        context_lens.data_ptr(), b, hq, hkv, d, float(scale), int(max_context_len), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(),
+    )
+    _check(status, "nvamd_paged_decode")
+    return out
+
+
+def kv_cache_write(key_states: torch.Tensor, value_states: torch.Tensor, key_cache: torch.Tensor,
+                   value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """cache_flat[slot_mapping[t]] = kv[t] for the K and the V cache of one layer."""
+    lib = load()
+    _bf16_cuda("key_states", key_states)
+    _bf16_cuda("value_states", value_states)
+    _require(key_states.shape == value_states.shape and key_states.dim() == 3, "k/v shape mismatch")
+    t, hkv, d = key_states.shape
+    _require(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    _require(key_cache.shape[-2:] == (hkv, d), f"kv shape mismatch: got {tuple(key_states.shape)}")
+    _require(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t and slot_mapping.is_cuda,
+             f"slot_mapping numel {slot_mapping.numel()} != total_tokens {t}")
+    num_slots = key_cache.numel() // (hkv * d)
+    status = lib.nvamd_kv_cache_write(
+        key_states.data_ptr(), _row_stride(key_states), value_states.data_ptr(), _row_stride(value_states),
+        key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.contiguous().data_ptr(), t, hkv, d, num_slots,
+        _stream(),
+    )
+    _check(status, "nvamd_kv_cache_write")
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                 positions: torch.Tensor, cos_sin: torch.Tensor, eps: float,
+                 v: torch.Tensor | None = None, key_cache: torch.Tensor | None = None,
+                 value_cache: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None) -> None:
+    """In place: q, k <- RoPE(RMSNorm_head(x) * w); optionally store post-RoPE k and v in the caches."""
+    lib = load()
+    _bf16_cuda("q", q)
+    _bf16_cuda("k", k)
+    _require(q.dim() == 3 and k.dim() == 3 and q.shape[0] == k.shape[0], "q/k must be [T, heads, D]")
+    t, hq, d = q.shape
+    hkv = k.shape[1]
+    _require(k.shape[2] == d, "q/k head_dim mismatch")
+    _require(q_weight.dtype == torch.bfloat16 and k_weight.dtype == torch.bfloat16, "norm weights must be bf16")
+    _require(q_weight.numel() == d and k_weight.numel() == d, "norm weights must have head_dim elements")
+    _require(positions.dtype == torch.int64 and positions.numel() == t and positions.is_cuda,
+             "positions must be int64 [T] on the device")
+    _require(cos_sin.dtype == torch.float32 and cos_sin.dim() == 2 and cos_sin.shape[1] == d and cos_sin.is_cuda,
+             "cos_sin must be fp32 [max_positions, head_dim]")
+    store = key_cache is not None
+    num_slots = 0
+    if store:
+        _require(v is not None and value_cache is not None and slot_mapping is not None, "store needs v, caches, slots")
+        _bf16_cuda("v", v)
+        _require(v.shape == k.shape, "k/v shape mismatch")
+        _require(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+        _require(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t, "slot_mapping must be int64 [T]")
+        num_slots = key_cache.numel() // (hkv * d)
+    status = lib.nvamd_qk_norm_rope(
+        q.data_ptr(), _row_stride(q), k.data_ptr(), _row_stride(k), _ptr(v), _row_stride(v) if store else 0,
+        q_weight.data_ptr(), k_weight.data_ptr(), positions.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0],
+        _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping.contiguous()) if store else None, num_slots,
+        t, hq, hkv, d, float(eps), _stream(),
+    )
+    _check(status, "nvamd_qk_norm_rope")

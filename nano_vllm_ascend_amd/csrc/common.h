@@ -1,0 +1,120 @@
+// Device helpers shared by the gfx950 kernels of the attention path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nvamd.h"
+
+namespace nvamd {
+
+using u32 = uint32_t;
+using u16 = uint16_t;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+
+constexpr int kHeadDim = 128;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// bf16 <-> fp32.  A bf16 is the top half of an fp32, so widening is a shift.
+__device__ __forceinline__ float bf16_lo(u32 x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi(u32 x) { return __uint_as_float(x & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(u16 x) { return __uint_as_float(((u32)x) << 16); }
+
+// Round two fp32 to bf16 (round-to-nearest-even, one v_cvt_pk_bf16_f32) and pack.
+__device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
+  bf16x2v r;
+  r[0] = (__bf16)lo;
+  r[1] = (__bf16)hi;
+  return __builtin_bit_cast(u32, r);
+}
+__device__ __forceinline__ u16 f32_to_bf16(float x) {
+  __bf16 r = (__bf16)x;
+  return __builtin_bit_cast(u16, r);
+}
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// acc + a.lo*b.lo + a.hi*b.hi with bf16 pairs and fp32 accumulation.
+__device__ __forceinline__ float dot2_bf16(u32 a, u32 b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a),
+                                         __builtin_bit_cast(bf16x2v, b), acc, false);
+}
+
+// Byte permutes: low halves of (a, b) -> (a.lo, b.lo); high halves -> (a.hi, b.hi).
+__device__ __forceinline__ u32 pair_lo(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ u32 pair_hi(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+// Cross-lane moves.  DPP control words (gfx9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // row_half_mirror (reverse within 8 lanes)
+constexpr int kDppMirror = 0x140;       // row_mirror (reverse within 16 lanes)
+constexpr int kDppRowRor8 = 0x128;      // row_ror:8 (lane i <- lane (i+8)%16 in a row)
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// ds_swizzle in bit mode: xor the lane id with 16 inside each 32-lane half.
+__device__ __forceinline__ float swizzle_xor16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 8 consecutive lanes of an aligned group; every lane of the group gets the sum.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  return v;
+}
+// Sum over 16 lanes (one DPP row).
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return v;
+}
+// Maximum over the whole wave for a value already uniform inside each aligned
+// group of 8 lanes.  The result is wave-uniform (it lives in an SGPR).
+__device__ __forceinline__ float wave_max_from_groups8(float v) {
+  v = fmaxf(v, dpp<kDppRowRor8>(v));
+  v = fmaxf(v, swizzle_xor16(v));
+  return fmaxf(readlane(v, 0), readlane(v, 32));
+}
+// Full 64-lane sum, wave-uniform result: reduce each 16-lane row, then add the 4 row sums.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = sum16(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
+__device__ __forceinline__ u32x4 ld16(const u16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
+__device__ __forceinline__ u32x4 ld16_stream(const u16 *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+__device__ __forceinline__ void st16(u16 *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }
+
+__host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+inline int log2_exact(int x) {
+  if (x <= 0 || (x & (x - 1)) != 0) return -1;
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NVAMD_OK : (int)e;
+}
+
+}  // namespace nvamd

@@ -1,0 +1,439 @@
+// GQA paged decode attention for gfx950 (replaces torch_npu._npu_paged_attention,
+// nv/layers/npu_paged_attention.py:27-100).
+//
+// Work decomposition (split-KV, one kernel):
+//   grid = (num_kv_heads, batch, max_parts); a workgroup of NW waves owns one
+//   (sequence b, kv head g, partition p) of PART = NW * CPW * 64 consecutive
+//   context tokens, for all GQA query heads that read kv head g, so every K/V
+//   byte is read from HBM once.  Each wave owns CPW chunks of 64 tokens.
+//   The partition index is the slowest grid dimension, so workgroups are
+//   dispatched partition by partition and the empty ones that a loose context
+//   bound adds (graph capture uses max_model_len) come last.
+//
+// Lane layout inside a wave (64 lanes): r = lane/8 picks token rows r and r+8
+// of each 16-row tile, c = lane%8 picks dims 8c..8c+7 and 64+8c..64+8c+7.
+// Eight lanes read one 256-byte K/V row as two whole 128-byte lines.
+//
+// Per 64-token chunk a wave issues all 32 of its 16-byte loads first (32 KB in
+// flight per wave); tiles past the wave's range re-read its last valid tile
+// (a cache hit, not HBM traffic) so the load stream stays branch free.  Then:
+//   QK:  v_dot2 over bf16 pairs for the whole chunk, 3-step DPP sum over 8 lanes;
+//   softmax: each 8-lane row group keeps its own running max, so a chunk
+//        needs no cross-lane max and no branch -- one rescale per chunk;
+//   PV:  the two rows a lane holds are paired per dim with v_perm, P is
+//        rounded to bf16 pairs, one v_dot2 adds both tokens' terms.
+// GQA 2 fills 2 of 16 rows of an MFMA tile, so the contraction stays on v_dot2
+// in the vector ALUs, which have ample headroom: the kernel is HBM bound.
+//
+// Multi-partition sequences: every workgroup publishes (max, sum, acc[128])
+// per head with agent-scope write-through stores, waits for them, and bumps an
+// arrival counter; the last to arrive reads the partials with agent-scope loads
+// and writes the output.  No L2 writeback or invalidate is needed.
+#include "common.h"
+
+namespace nvamd {
+namespace {
+
+constexpr int kPartFloats = 132;  // max, sum, 128 accumulators, 2 pad (16-byte rows)
+// Arrival counters live in a fixed-size region at the front of the workspace so
+// calls with different batch sizes or context bounds never place partial
+// results where another call expects a zero counter.
+constexpr int kCounterSlots = 16384;
+constexpr size_t kCounterBytes = kCounterSlots * sizeof(int);
+constexpr int kMinPart = 256;  // smallest partition any launch uses (sizes the workspace)
+
+struct DecodeArgs {
+  u16 *out;
+  int64_t out_stride;
+  const u16 *q;
+  int64_t q_stride;
+  const u16 *k_cache;
+  const u16 *v_cache;
+  const int32_t *block_tables;
+  const int32_t *context_lens;
+  float *partials;
+  int *counters;
+  int bt_stride;
+  int bt_width;
+  int num_blocks;
+  int num_kv_heads;
+  int bs_log2;
+  int max_parts;
+  int max_ctx;
+  float scale_log2e;
+};
+
+struct KVTile {
+  u32x4 ka0, ka1, kb0, kb1, va0, va1, vb0, vb1;
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void store_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int GQA, int NW, int CPW>
+__global__ void __launch_bounds__(NW * 64)
+paged_decode_kernel(DecodeArgs a) {
+  constexpr int D = kHeadDim;
+  constexpr int WT = CPW * 64;  // tokens per wave
+  constexpr int PART = NW * WT;
+
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const int p = blockIdx.z;
+  const int hkv = a.num_kv_heads;
+
+  int ctx = a.context_lens[b];
+  ctx = min(ctx, min(a.max_ctx, a.bt_width << a.bs_log2));
+  ctx = max(ctx, 0);
+  const int n_parts = ceil_div(ctx, PART);
+  if (p >= (n_parts > 0 ? n_parts : 1)) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
+  const int r = lane >> 3;
+  const int c = lane & 7;
+
+  __shared__ float s_o[NW][GQA][8][D];
+  __shared__ float s_l[NW][GQA][8];
+  __shared__ float s_m[NW][GQA][8];
+  __shared__ float s_f[NW][GQA][8];
+  __shared__ float s_pm[64][GQA];  // merge stage: per-partition factors
+  __shared__ float s_pl[GQA];
+  __shared__ int s_last;
+
+  // Query rows of the GQA group, as bf16 pairs for v_dot2.
+  u32x4 qr[GQA][2];
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) {
+    const u16 *qp = a.q + (int64_t)b * a.q_stride + (int64_t)(g * GQA + j) * D + 8 * c;
+    qr[j][0] = ld16(qp);
+    qr[j][1] = ld16(qp + 64);
+  }
+
+  float m[GQA], l[GQA], o[GQA][16];
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[j][i] = 0.f;
+  }
+
+  const int t_begin = p * PART + w * WT;
+  const int t_end = min(t_begin + WT, ctx);
+  const int bs_mask = (1 << a.bs_log2) - 1;
+  const int64_t row_elems = (int64_t)hkv * D;  // elements between consecutive tokens
+  const int64_t step8 = 8 * row_elems;
+  const int32_t *bt_row = a.block_tables + (int64_t)b * a.bt_stride;
+
+  if (t_begin < t_end) {
+    const int last_tile = (t_end - 1) & ~15;
+#pragma unroll 1
+    for (int tc = t_begin; tc < t_end; tc += 64) {
+      KVTile T[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t0 = min(tc + 16 * i, last_tile);
+        int blk = bt_row[t0 >> a.bs_log2];
+        blk = min(max(blk, 0), a.num_blocks - 1);  // never leave the pool
+        const int64_t slot = ((int64_t)blk << a.bs_log2) + (t0 & bs_mask) + r;
+        const int64_t off = slot * row_elems + (int64_t)g * D + 8 * c;
+        const u16 *kp = a.k_cache + off;
+        const u16 *vp = a.v_cache + off;
+        T[i].ka0 = ld16(kp);
+        T[i].ka1 = ld16(kp + 64);
+        T[i].kb0 = ld16(kp + step8);
+        T[i].kb1 = ld16(kp + step8 + 64);
+        T[i].va0 = ld16(vp);
+        T[i].va1 = ld16(vp + 64);
+        T[i].vb0 = ld16(vp + step8);
+        T[i].vb1 = ld16(vp + step8 + 64);
+      }
+
+      // QK for the chunk: s[tile][row a/b][head]
+      float s[4][2][GQA];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+          float sa = 0.f, sb = 0.f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sa = dot2_bf16(qr[j][0][e], T[i].ka0[e], sa);
+            sb = dot2_bf16(qr[j][0][e], T[i].kb0[e], sb);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sa = dot2_bf16(qr[j][1][e], T[i].ka1[e], sa);
+            sb = dot2_bf16(qr[j][1][e], T[i].kb1[e], sb);
+          }
+          s[i][0][j] = sa;
+          s[i][1][j] = sb;
+        }
+      }
+      bool ok[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ok[i][0] = (tc + 16 * i + r) < t_end;
+        ok[i][1] = (tc + 16 * i + 8 + r) < t_end;
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+          const float sa = sum8(s[i][0][j]) * a.scale_log2e;
+          const float sb = sum8(s[i][1][j]) * a.scale_log2e;
+          s[i][0][j] = ok[i][0] ? sa : -INFINITY;
+          s[i][1][j] = ok[i][1] ? sb : -INFINITY;
+        }
+      }
+
+      // Online softmax, one step per chunk, per 8-lane row group.
+      u32 pp[4][GQA];
+#pragma unroll
+      for (int j = 0; j < GQA; ++j) {
+        float cm = m[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cm = fmaxf(cm, fmaxf(s[i][0][j], s[i][1][j]));
+        const float ref = cm == -INFINITY ? 0.f : cm;  // a group with no valid row yet
+        const float alpha = fast_exp2(m[j] - ref);
+        m[j] = cm;
+        float add = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pp[i][j] = pack_bf16x2(fast_exp2(s[i][0][j] - ref), fast_exp2(s[i][1][j] - ref));
+          add += bf16_lo(pp[i][j]) + bf16_hi(pp[i][j]);
+        }
+        l[j] = l[j] * alpha + add;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[j][e] *= alpha;
+      }
+
+      // Rows past the context may hold stale bits (NaN * 0 = NaN): zero their V.
+      if (tc + 64 > t_end) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (!ok[i][0]) { T[i].va0 = z; T[i].va1 = z; }
+          if (!ok[i][1]) { T[i].vb0 = z; T[i].vb1 = z; }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const u32 lo0 = pair_lo(T[i].va0[e], T[i].vb0[e]);
+          const u32 hi0 = pair_hi(T[i].va0[e], T[i].vb0[e]);
+          const u32 lo1 = pair_lo(T[i].va1[e], T[i].vb1[e]);
+          const u32 hi1 = pair_hi(T[i].va1[e], T[i].vb1[e]);
+#pragma unroll
+          for (int j = 0; j < GQA; ++j) {
+            o[j][2 * e] = dot2_bf16(pp[i][j], lo0, o[j][2 * e]);
+            o[j][2 * e + 1] = dot2_bf16(pp[i][j], hi0, o[j][2 * e + 1]);
+            o[j][8 + 2 * e] = dot2_bf16(pp[i][j], lo1, o[j][8 + 2 * e]);
+            o[j][8 + 2 * e + 1] = dot2_bf16(pp[i][j], hi1, o[j][8 + 2 * e + 1]);
+          }
+        }
+      }
+    }
+  }
+
+  // Workgroup merge of the NW * 8 row-group states of each head.
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) {
+    float *dst = &s_o[w][j][r][0];
+    // o[j][0..7] hold dims 8c..8c+7, o[j][8..15] hold dims 64+8c..64+8c+7
+    *reinterpret_cast<f32x4 *>(dst + 8 * c) = f32x4{o[j][0], o[j][1], o[j][2], o[j][3]};
+    *reinterpret_cast<f32x4 *>(dst + 8 * c + 4) = f32x4{o[j][4], o[j][5], o[j][6], o[j][7]};
+    *reinterpret_cast<f32x4 *>(dst + 64 + 8 * c) = f32x4{o[j][8], o[j][9], o[j][10], o[j][11]};
+    *reinterpret_cast<f32x4 *>(dst + 64 + 8 * c + 4) = f32x4{o[j][12], o[j][13], o[j][14], o[j][15]};
+    if (c == 0) {
+      s_l[w][j][r] = l[j];
+      s_m[w][j][r] = m[j];
+    }
+  }
+  __syncthreads();
+  if (tid < NW * GQA * 8) {
+    const int ww = tid / (GQA * 8);
+    const int j = (tid / 8) % GQA;
+    const int rr = tid % 8;
+    float M = -INFINITY;
+    for (int x = 0; x < NW; ++x)
+      for (int y = 0; y < 8; ++y) M = fmaxf(M, s_m[x][j][y]);
+    const float mv = s_m[ww][j][rr];
+    s_f[ww][j][rr] = mv == -INFINITY ? 0.f : fast_exp2(mv - M);
+    if (ww == 0 && rr == 0) s_pl[j] = M;
+  }
+  __syncthreads();
+
+  float *part_base = a.partials + (((int64_t)b * hkv + g) * a.max_parts) * GQA * kPartFloats;
+  u16 *out_base = a.out + (int64_t)b * a.out_stride + (int64_t)g * GQA * D;
+
+  for (int idx = tid; idx < GQA * D; idx += NW * 64) {
+    const int j = idx / D;
+    const int d = idx % D;
+    float acc = 0.f, ls = 0.f;
+#pragma unroll
+    for (int x = 0; x < NW; ++x)
+#pragma unroll
+      for (int y = 0; y < 8; ++y) {
+        const float f = s_f[x][j][y];
+        acc += f * s_o[x][j][y][d];
+        ls += f * s_l[x][j][y];
+      }
+    if (n_parts <= 1) {
+      out_base[j * D + d] = f32_to_bf16(ls > 0.f ? acc / ls : 0.f);
+    } else {
+      float *pr = part_base + ((int64_t)p * GQA + j) * kPartFloats;
+      store_agent(pr + 2 + d, acc);
+      if (d == 0) {
+        store_agent(pr, s_pl[j]);
+        store_agent(pr + 1, ls);
+      }
+    }
+  }
+  if (n_parts <= 1) return;
+
+  // Publish: wait until this workgroup's write-through stores are complete,
+  // then count the arrival.  The last workgroup of (b, g) merges.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keep the stores above the wait
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int *counter = a.counters + (int64_t)b * hkv + g;
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == n_parts - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  if (tid < n_parts * GQA) {
+    const int pp2 = tid / GQA;
+    const int j = tid % GQA;
+    const float *pr = part_base + ((int64_t)pp2 * GQA + j) * kPartFloats;
+    s_pm[pp2][j] = load_agent(pr);
+  }
+  __syncthreads();
+  if (tid < GQA) {
+    float M = -INFINITY;
+    for (int x = 0; x < n_parts; ++x) M = fmaxf(M, s_pm[x][tid]);
+    s_pl[tid] = M;
+  }
+  __syncthreads();
+  if (tid < n_parts * GQA) {
+    const int pp2 = tid / GQA;
+    const int j = tid % GQA;
+    const float mp = s_pm[pp2][j];
+    s_pm[pp2][j] = mp == -INFINITY ? 0.f : fast_exp2(mp - s_pl[j]);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < GQA * D; idx += NW * 64) {
+    const int j = idx / D;
+    const int d = idx % D;
+    float num = 0.f, den = 0.f;
+    for (int x = 0; x < n_parts; ++x) {
+      const float *pr = part_base + ((int64_t)x * GQA + j) * kPartFloats;
+      const float f = s_pm[x][j];
+      num += f * load_agent(pr + 2 + d);
+      den += f * load_agent(pr + 1);
+    }
+    out_base[j * D + d] = f32_to_bf16(den > 0.f ? num / den : 0.f);
+  }
+  if (tid == 0) {  // leave the workspace ready for the next call
+    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <int GQA, int NW, int CPW>
+int launch(DecodeArgs a, int batch, hipStream_t stream) {
+  constexpr int PART = NW * CPW * 64;
+  a.max_parts = ceil_div(a.max_ctx, PART);
+  if (a.max_parts > 64) return NVAMD_EUNSUPPORTED;  // merge stage holds <= 64 partitions
+  dim3 grid(a.num_kv_heads, batch, a.max_parts);
+  hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW>), grid, dim3(NW * 64), 0, stream, a);
+  return launch_status();
+}
+
+template <int GQA>
+int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
+  // 256-token partitions (measured best on MI355X for 32 x ~1.3k contexts);
+  // longer ones only when the context bound would exceed 64 of them.
+  (void)batch;
+  int cpw = 1;
+  while (ceil_div(a.max_ctx, 256 * cpw) > 64) cpw *= 2;
+  switch (cpw) {
+    case 1: return launch<GQA, 4, 1>(a, batch, stream);
+    case 2: return launch<GQA, 4, 2>(a, batch, stream);
+    case 4: return launch<GQA, 4, 4>(a, batch, stream);
+    case 8: return launch<GQA, 4, 8>(a, batch, stream);
+    default: return NVAMD_EUNSUPPORTED;
+  }
+}
+
+}  // namespace
+}  // namespace nvamd
+
+using namespace nvamd;
+
+extern "C" size_t nvamd_paged_decode_workspace_size(int max_batch, int num_heads, int num_kv_heads,
+                                                    int max_context_len) {
+  if (max_batch <= 0 || num_kv_heads <= 0 || num_heads <= 0 || max_context_len <= 0) return 0;
+  const int gqa = num_heads / num_kv_heads;
+  const size_t parts = (size_t)ceil_div(max_context_len, kMinPart);
+  const size_t units = (size_t)max_batch * num_kv_heads;
+  return kCounterBytes + units * parts * gqa * kPartFloats * sizeof(float);
+}
+
+extern "C" int nvamd_paged_decode(void *out, int64_t out_stride, const void *q, int64_t q_stride,
+                                  const void *k_cache, const void *v_cache, int num_blocks, int block_size,
+                                  const int32_t *block_tables, int bt_stride, int bt_width,
+                                  const int32_t *context_lens, int batch, int num_heads, int num_kv_heads,
+                                  int head_dim, float scale, int max_context_len, void *workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+  if (batch == 0) return NVAMD_OK;
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens) return NVAMD_EINVAL;
+  if (batch < 0 || num_blocks <= 0 || num_kv_heads <= 0 || num_heads <= 0 || bt_width <= 0 ||
+      bt_stride < bt_width || max_context_len <= 0)
+    return NVAMD_EINVAL;
+  if (head_dim != kHeadDim) return NVAMD_EUNSUPPORTED;
+  if (num_heads % num_kv_heads != 0) return NVAMD_EINVAL;
+  const int bs_log2 = log2_exact(block_size);
+  if (bs_log2 < 4) return NVAMD_EUNSUPPORTED;
+  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || (q_stride % 8) != 0 ||
+      (out_stride % 8) != 0 || q_stride < (int64_t)num_heads * head_dim || out_stride < (int64_t)num_heads * head_dim)
+    return NVAMD_EINVAL;
+  if ((int64_t)batch * num_kv_heads > kCounterSlots || batch > 65535) return NVAMD_EUNSUPPORTED;
+  const size_t need = nvamd_paged_decode_workspace_size(batch, num_heads, num_kv_heads, max_context_len);
+  if (!workspace || workspace_bytes < need) return NVAMD_EWORKSPACE;
+
+  DecodeArgs a;
+  a.out = static_cast<u16 *>(out);
+  a.out_stride = out_stride;
+  a.q = static_cast<const u16 *>(q);
+  a.q_stride = q_stride;
+  a.k_cache = static_cast<const u16 *>(k_cache);
+  a.v_cache = static_cast<const u16 *>(v_cache);
+  a.block_tables = block_tables;
+  a.context_lens = context_lens;
+  a.counters = static_cast<int *>(workspace);
+  a.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) + kCounterBytes);
+  a.bt_stride = bt_stride;
+  a.bt_width = bt_width;
+  a.num_blocks = num_blocks;
+  a.num_kv_heads = num_kv_heads;
+  a.bs_log2 = bs_log2;
+  a.max_ctx = max_context_len;
+  a.max_parts = 0;
+  a.scale_log2e = scale * kLog2e;
+
+  switch (num_heads / num_kv_heads) {
+    case 1: return dispatch<1>(a, batch, stream);
+    case 2: return dispatch<2>(a, batch, stream);
+    case 4: return dispatch<4>(a, batch, stream);
+    default: return NVAMD_EUNSUPPORTED;
+  }
+}

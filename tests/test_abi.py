@@ -1,0 +1,33 @@
+"""CPU checks of the C ABI: the library loads and exports every declared entry point."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+from nano_vllm_ascend_amd import _C
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nvamd.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"\b(nvamd_\w+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == set(_C.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _C.load()
+    for name in declared_symbols():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_host_only_entry_points():
+    assert _C.version() >= 1
+    small = _C.paged_decode_workspace_size(4, 16, 8, 512)
+    big = _C.paged_decode_workspace_size(32, 16, 8, 4096)
+    assert 0 < small < big
+    assert _C.paged_decode_workspace_size(0, 16, 8, 512) == 0

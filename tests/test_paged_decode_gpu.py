@@ -1,0 +1,153 @@
+"""Parity of the HIP paged decode kernel with the fp32 oracle (max-abs <= 2e-2 in bf16)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nano_vllm_ascend_amd import _C
+from nano_vllm_ascend_amd import workloads as W
+from oracle.attention_ref import paged_decode_ref
+
+TOL = 2e-2  # max-abs error allowed against the fp32 reference of the same paged semantics
+SCALE = W.HEAD_DIM ** -0.5
+
+
+def run_decode(q, kc, vc, block_tables, context_lens, max_ctx, out=None, ws=None):
+    out = torch.empty_like(q) if out is None else out
+    if ws is None:
+        ws = _C.alloc_paged_decode_workspace(q.shape[0], q.shape[1], kc.shape[2], max_ctx, q.device)
+    _C.paged_decode(out, q, kc, vc, block_tables, context_lens, SCALE, max_ctx, ws)
+    return out
+
+
+def check(work, layer=0, max_ctx=None):
+    max_ctx = max_ctx or max(work.context_lens_list)
+    out = run_decode(work.q, work.key_cache[layer], work.value_cache[layer], work.block_tables,
+                     work.context_lens, max_ctx)
+    torch.cuda.synchronize()
+    ref = paged_decode_ref(work.q, work.key_cache[layer], work.value_cache[layer], work.block_tables,
+                           work.context_lens, SCALE)
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= TOL, f"max-abs {err:.4g} > {TOL}"
+    return err
+
+
+@pytest.mark.gpu
+def test_decode_single_layer_batch4(device):
+    for seed in range(3):
+        check(W.decode_single(device, seed=seed))
+
+
+@pytest.mark.gpu
+def test_decode_step_batch32(device):
+    work = W.decode_step(device, seed=0)
+    check(work)
+    # a larger bound than needed only adds empty workgroups
+    check(work, max_ctx=4096)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 127, 128, 129, 255, 256, 257, 511, 512, 513, 1023, 1024, 1025,
+                                 2047, 2048, 2049, 4096])
+def test_decode_edge_lengths(device, ctx):
+    work = W.make_decode(3, 0, 0, 160, seed=ctx, device=device, context_lens=[ctx, max(1, ctx // 3), 1])
+    check(work)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads", [(8, 8), (16, 8), (16, 4)])
+def test_decode_gqa_groups(device, heads):
+    hq, hkv = heads
+    work = W.make_decode(5, 1, 700, 64, seed=7, device=device, num_heads=hq, num_kv_heads=hkv)
+    check(work)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bs", [16, 32, 64, 256])
+def test_decode_block_sizes(device, bs):
+    work = W.make_decode(4, 1, 600, 256, seed=bs, device=device, block_size=bs)
+    check(work)
+
+
+@pytest.mark.gpu
+def test_decode_ignores_stale_rows_past_context(device):
+    """Unwritten rows of the last block may hold NaN bit patterns; they must not reach the output."""
+    work = W.make_decode(4, 1, 300, 16, seed=3, device=device)
+    bs = work.key_cache.shape[2]
+    bt = work.block_tables.cpu()
+    for i, c in enumerate(work.context_lens_list):
+        last = int(bt[i, (c - 1) // bs])
+        off = c % bs
+        if off:
+            work.key_cache[0, last, off:] = float("nan")
+            work.value_cache[0, last, off:] = float("inf")
+    err = check(work)
+    assert err == err  # not NaN
+
+
+@pytest.mark.gpu
+def test_decode_workspace_reused_across_shapes(device):
+    """Counters are left at zero, so one workspace serves calls of different batch and bound."""
+    big = W.decode_step(device, seed=1)
+    small = W.decode_single(device, seed=1)
+    ws = _C.alloc_paged_decode_workspace(32, 16, 8, 4096, device)
+    for _ in range(2):
+        for work, mc in ((big, 4096), (small, 512), (big, 2304)):
+            out = run_decode(work.q, work.key_cache[0], work.value_cache[0], work.block_tables, work.context_lens,
+                             mc, ws=ws)
+            torch.cuda.synchronize()
+            ref = paged_decode_ref(work.q, work.key_cache[0], work.value_cache[0], work.block_tables,
+                                   work.context_lens, SCALE)
+            assert (out.float().cpu() - ref).abs().max().item() <= TOL
+    counters = ws[: 16384 * 4].view(torch.int32)
+    assert int(counters.abs().sum()) == 0
+
+
+@pytest.mark.gpu
+def test_decode_strided_query_view(device):
+    """q may be a view into a fused [B, (Hq+2Hkv)*D] projection; out may be strided too."""
+    work = W.decode_single(device, seed=5)
+    b = work.q.shape[0]
+    qkv = torch.zeros(b, 32 * 128, dtype=torch.bfloat16, device=device)
+    qkv[:, : 16 * 128] = work.q.reshape(b, -1)
+    qv = qkv[:, : 16 * 128].view(b, 16, 128)
+    outbuf = torch.zeros(b, 24 * 128, dtype=torch.bfloat16, device=device)
+    outv = outbuf[:, 8 * 128 :].view(b, 16, 128)
+    run_decode(qv, work.key_cache[0], work.value_cache[0], work.block_tables, work.context_lens, 512, out=outv)
+    torch.cuda.synchronize()
+    ref = paged_decode_ref(work.q, work.key_cache[0], work.value_cache[0], work.block_tables, work.context_lens,
+                           SCALE)
+    assert (outv.float().cpu() - ref).abs().max().item() <= TOL
+    assert int(outbuf[:, : 8 * 128].abs().sum()) == 0  # nothing written outside the view
+
+
+@pytest.mark.gpu
+def test_decode_graph_replays_read_device_context_lens(device):
+    """A captured launch replays with new context_lens / q / tables and no host-side update."""
+    work = W.decode_step(device, seed=2)
+    b = work.q.shape[0]
+    q = work.q.clone()
+    bt = work.block_tables.clone()
+    cl = work.context_lens.clone()
+    out = torch.empty_like(q)
+    ws = _C.alloc_paged_decode_workspace(b, 16, 8, 4096, device)
+    kc, vc = work.key_cache[0], work.value_cache[0]
+    run_decode(q, kc, vc, bt, cl, 4096, out=out, ws=ws)  # warm-up outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_decode(q, kc, vc, bt, cl, 4096, out=out, ws=ws)
+    gen = torch.Generator().manual_seed(11)
+    for rep in range(4):
+        new_ctx = torch.randint(1, 2305, (b,), generator=gen, dtype=torch.int32)
+        new_ctx = torch.minimum(new_ctx, torch.tensor(work.context_lens_list, dtype=torch.int32))
+        cl.copy_(new_ctx.to(device))
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(device))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = paged_decode_ref(q, kc, vc, bt, cl, SCALE)
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= TOL, f"replay {rep}: {err}"
+        eager = run_decode(q, kc, vc, bt, cl, 4096, ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(eager, out), f"replay {rep} differs from eager"
