@@ -111,6 +111,72 @@ int nvamd_qk_norm_rope(void *q, int64_t q_stride,
                        int head_dim, float eps,
                        hipStream_t stream);
 
+/* ------------------------------------------------------------------------- */
+/* P3: causal varlen prefill attention (bf16 MFMA).                           */
+/* Replaces torch_npu.npu_fused_infer_attention_score as called at            */
+/* nv/layers/npu_prefill_attention.py:98-112 (dense route) and :66-96 (paged, */
+/* prefix-hit route), TND layout, scale = head_dim^-0.5, GQA h -> h/(Hq/Hkv). */
+/* cu_seqlens_q: int32 [n_seqs+1] on the device (the reference passes the     */
+/* cumulative ends without the leading 0 as a host list).                     */
+/* dense: k/v hold the same tokens as q; row i of a sequence sees keys 0..i.  */
+/* paged: keys come from the cache through block_tables; kv_lens (device,     */
+/*   per sequence -- the reference's per-layer context_lens.tolist()) gives   */
+/*   each sequence's key count; query row r of a q_len-row sequence sees keys */
+/*   0..kv_len-q_len+r (causal, bottom-right aligned).                        */
+/* max_q_len bounds every q_len (it sizes the grid).                          */
+/* ------------------------------------------------------------------------- */
+int nvamd_varlen_prefill(void *out, int64_t out_stride,
+                         const void *q, int64_t q_stride,
+                         const void *k, int64_t k_stride,
+                         const void *v, int64_t v_stride,
+                         const int32_t *cu_seqlens_q, int n_seqs, int max_q_len,
+                         int num_heads, int num_kv_heads, int head_dim,
+                         float scale, hipStream_t stream);
+
+int nvamd_paged_prefill(void *out, int64_t out_stride,
+                        const void *q, int64_t q_stride,
+                        const void *k_cache, const void *v_cache,
+                        int num_blocks, int block_size,
+                        const int32_t *block_tables, int bt_stride, int bt_width,
+                        const int32_t *cu_seqlens_q, const int32_t *kv_lens,
+                        int n_seqs, int max_q_len,
+                        int num_heads, int num_kv_heads, int head_dim,
+                        float scale, hipStream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* P1: ragged-batch packing.                                                  */
+/* Replaces BlockManager.get_block_tables_tensor / get_context_lens_tensor /  */
+/* get_slot_mapping (nv/npu/block_manager.py:207-250; the per-token Python    */
+/* slot loop and one H2D copy per table row) and the input build of           */
+/* ModelRunner._prepare_prefill_inputs (nv/model_runner.py:169-197) and       */
+/* ModelRunner.decode (nv/model_runner.py:245-258).                           */
+/* desc: int32 [5][batch] on the device = mirror row, start position, query   */
+/*   length, table length (blocks), context length of each sequence.         */
+/* updates: int32 [num_updates][3] = (mirror row, column, block id) entries   */
+/*   of the device block-table mirror [mirror_rows, mirror_stride] that       */
+/*   changed since the last call; applied before anything is read.  At most   */
+/*   one entry per (row, column).                                             */
+/* Outputs (any may be NULL to skip):                                         */
+/*   block_tables[i, c] = c < table_len_i ? mirror[row_i, c] : 0, c < bt_width*/
+/*   context_lens[i]; cu_seqlens[0..batch] (cumulative query lengths);        */
+/*   last_token_indices[i] = cu_seqlens[i+1] - 1;                             */
+/*   for token k of sequence i (t = cu_seqlens[i] + k, pos = start_i + k):    */
+/*     positions[t] = pos;                                                    */
+/*     slot_mapping[t] = mirror[row_i, pos / bs] * bs + pos % bs (-1 if the   */
+/*       table does not reach pos);                                           */
+/*     input_ids[t] = token_ids[t] (int32 -> int64).                          */
+/* ------------------------------------------------------------------------- */
+int nvamd_pack_batch(const int32_t *desc, int batch,
+                     const int32_t *updates, int num_updates,
+                     const int32_t *token_ids,
+                     int32_t *mirror, int mirror_stride, int mirror_rows,
+                     int block_size,
+                     int32_t *block_tables, int bt_stride, int bt_width,
+                     int32_t *context_lens, int64_t *slot_mapping,
+                     int64_t *positions, int32_t *cu_seqlens,
+                     int64_t *last_token_indices, int64_t *input_ids,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

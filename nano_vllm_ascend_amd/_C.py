@@ -38,6 +38,21 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_i64, _c_ptr],
     ),
+    "nvamd_pack_batch": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_ptr,
+         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "nvamd_varlen_prefill": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_float, _c_ptr],
+    ),
+    "nvamd_paged_prefill": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_ptr, _c_ptr,
+         _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_ptr],
+    ),
     "nvamd_qk_norm_rope": (
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr,
@@ -213,3 +228,78 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_wei
         t, hq, hkv, d, float(eps), _stream(),
     )
     _check(status, "nvamd_qk_norm_rope")
+
+
+def pack_batch(desc: torch.Tensor, batch: int, updates: torch.Tensor | None, num_updates: int,
+               token_ids: torch.Tensor | None, mirror: torch.Tensor, block_size: int,
+               block_tables: torch.Tensor | None = None, context_lens: torch.Tensor | None = None,
+               slot_mapping: torch.Tensor | None = None, positions: torch.Tensor | None = None,
+               cu_seqlens: torch.Tensor | None = None, last_token_indices: torch.Tensor | None = None,
+               input_ids: torch.Tensor | None = None) -> None:
+    """Expand per-sequence descriptors into the packed-batch metadata on the GPU (see nvamd.h)."""
+    lib = load()
+    _require(desc.dtype == torch.int32 and desc.is_cuda and desc.numel() >= 5 * batch, "desc must be int32 [5, B]")
+    _require(mirror.dtype == torch.int32 and mirror.dim() == 2 and mirror.is_contiguous(), "mirror must be int32 2-D")
+    if block_tables is not None:
+        _require(block_tables.dtype == torch.int32 and block_tables.stride(1) == 1 and block_tables.shape[0] >= batch,
+                 "block_tables must be int32 [B, W] with dense rows")
+    for name, t, dt in (("context_lens", context_lens, torch.int32), ("slot_mapping", slot_mapping, torch.int64),
+                        ("positions", positions, torch.int64), ("cu_seqlens", cu_seqlens, torch.int32),
+                        ("last_token_indices", last_token_indices, torch.int64),
+                        ("input_ids", input_ids, torch.int64)):
+        if t is not None:
+            _require(t.dtype == dt and t.is_cuda and t.is_contiguous(), f"{name} must be a contiguous {dt} GPU tensor")
+    status = lib.nvamd_pack_batch(
+        desc.data_ptr(), batch, _ptr(updates), num_updates, _ptr(token_ids), mirror.data_ptr(), mirror.shape[1],
+        mirror.shape[0], block_size, _ptr(block_tables), block_tables.stride(0) if block_tables is not None else 0,
+        block_tables.shape[1] if block_tables is not None else 0, _ptr(context_lens), _ptr(slot_mapping),
+        _ptr(positions), _ptr(cu_seqlens), _ptr(last_token_indices), _ptr(input_ids), _stream(),
+    )
+    _check(status, "nvamd_pack_batch")
+
+
+def varlen_prefill(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                   max_q_len: int, scale: float) -> torch.Tensor:
+    """Dense causal varlen attention: q/out [T, Hq, 128], k/v [T, Hkv, 128], cu_seqlens_q int32 [B+1] (device)."""
+    lib = load()
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+        _bf16_cuda(name, t)
+        _require(t.dim() == 3, f"{name} must be [T, heads, D]")
+    _require(out.shape == q.shape, "q/out shape mismatch")
+    _require(k.shape == v.shape and k.shape[0] == q.shape[0], f"k/v token mismatch: q={tuple(q.shape)} "
+             f"k={tuple(k.shape)} v={tuple(v.shape)}")
+    _require(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.is_cuda and cu_seqlens_q.is_contiguous(),
+             "cu_seqlens_q must be int32 on the device")
+    n_seqs = cu_seqlens_q.numel() - 1
+    status = lib.nvamd_varlen_prefill(
+        out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), k.data_ptr(), _row_stride(k),
+        v.data_ptr(), _row_stride(v), cu_seqlens_q.data_ptr(), n_seqs, int(max_q_len), q.shape[1], k.shape[1],
+        q.shape[2], float(scale), _stream(),
+    )
+    _check(status, "nvamd_varlen_prefill")
+    return out
+
+
+def paged_prefill(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                  block_tables: torch.Tensor, cu_seqlens_q: torch.Tensor, kv_lens: torch.Tensor, max_q_len: int,
+                  scale: float) -> torch.Tensor:
+    """Prefix-hit prefill: queries are the last q_len of kv_len positions, keys read through the cache pages."""
+    lib = load()
+    for name, t in (("q", q), ("out", out), ("key_cache", key_cache), ("value_cache", value_cache)):
+        _bf16_cuda(name, t)
+    _require(out.shape == q.shape and q.dim() == 3, "q/out shape mismatch")
+    _require(key_cache.dim() == 4 and key_cache.shape == value_cache.shape, "key/value cache shape mismatch")
+    _require(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    _require(block_tables.dtype == torch.int32 and block_tables.stride(1) == 1, "block_tables must be int32 [B, W]")
+    _require(cu_seqlens_q.dtype == torch.int32 and kv_lens.dtype == torch.int32 and kv_lens.is_cuda,
+             "cu_seqlens_q / kv_lens must be int32 on the device")
+    nb, bs, hkv, d = key_cache.shape
+    n_seqs = cu_seqlens_q.numel() - 1
+    _require(kv_lens.numel() >= n_seqs and block_tables.shape[0] >= n_seqs, "per-sequence metadata too short")
+    status = lib.nvamd_paged_prefill(
+        out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), key_cache.data_ptr(), value_cache.data_ptr(),
+        nb, bs, block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1], cu_seqlens_q.data_ptr(),
+        kv_lens.data_ptr(), n_seqs, int(max_q_len), q.shape[1], hkv, d, float(scale), _stream(),
+    )
+    _check(status, "nvamd_paged_prefill")
+    return out

@@ -1,0 +1,342 @@
+// Causal varlen prefill attention on bf16 MFMA for gfx950 (replaces
+// torch_npu.npu_fused_infer_attention_score, nv/layers/npu_prefill_attention.py:41-113).
+//
+// Two routes share one kernel:
+//   dense  K/V are the packed activations of the same tokens (q_len == kv_len),
+//          row i of a sequence sees keys 0..i           (sparse_mode=3 route);
+//   paged  K/V are read through the block table from the paged cache, the
+//          queries are the last q_len positions of kv_len, and query row r
+//          sees keys 0..kv_len-q_len+r (bottom-right causal; prefix-hit route).
+//
+// Workgroup = 4 waves = one kv head g, its GQA query heads, and a tile of
+// BQ = 128/GQA query tokens; wave w owns 32 query rows of one head.
+// Per 64-key tile:
+//   S^T[64 keys x 32 queries] = K . Q^T  with v_mfma_f32_32x32x16_bf16
+//        (A = K rows from LDS, B = Q rows kept in registers for the whole loop).
+//        In this layout a lane owns ONE query column, so the softmax max/sum
+//        of a query is in-lane plus one exchange with lane^32.
+//   O^T[128 dims x 32 queries] += V^T . P^T
+//        The contraction index can be permuted as long as both operands agree:
+//        taking the k-slots in the order the S^T accumulator already holds its
+//        rows makes P^T a register-only repack (no lane movement); V^T is read
+//        from a transposed LDS copy with two 8-byte reads per operand.
+// Query tiles with the most keys dispatch first (tile index is the slowest
+// grid dimension, reversed); K/V of the next tile are loaded into registers
+// while the current tile's MFMAs run.
+#include "common.h"
+
+namespace nvamd {
+namespace {
+
+constexpr int kBK = 64;            // keys per tile
+constexpr int kKStride = 136;      // LDS row stride (elements) of the K tile: 272 B, spreads banks
+constexpr int kVtStride = 68;      // LDS row stride (elements) of the transposed V tile: 34 dwords
+
+struct PrefillArgs {
+  u16 *out;
+  int64_t out_stride;
+  const u16 *q;
+  int64_t q_stride;
+  const u16 *k;
+  int64_t k_stride;
+  const u16 *v;
+  int64_t v_stride;
+  const u16 *k_cache;
+  const u16 *v_cache;
+  const int32_t *block_tables;
+  const int32_t *cu_seqlens_q;
+  const int32_t *kv_lens;
+  int bt_stride;
+  int bt_width;
+  int num_blocks;
+  int bs_log2;
+  int num_kv_heads;
+  int max_q_tiles;
+  float scale_log2e;
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8v a, bf16x8v b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int GQA, bool PAGED>
+__global__ void __launch_bounds__(256)
+prefill_kernel(PrefillArgs a) {
+  constexpr int D = kHeadDim;
+  constexpr int BQ = 128 / GQA;     // query tokens per workgroup
+  constexpr int WPH = 4 / GQA;      // waves per query head
+
+  const int g = blockIdx.x;
+  const int s = blockIdx.y;
+  const int qt = a.max_q_tiles - 1 - (int)blockIdx.z;
+  const int q_start = a.cu_seqlens_q[s];
+  const int q_len = a.cu_seqlens_q[s + 1] - q_start;
+  if (qt * BQ >= q_len) return;
+  int kv_len = PAGED ? a.kv_lens[s] : q_len;
+  if (PAGED) kv_len = min(kv_len, a.bt_width << a.bs_log2);
+  const int offset = kv_len - q_len;  // query row r sees keys 0..offset+r
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = lane >> 5;        // lane half
+  const int n = lane & 31;         // this lane's query column
+  const int j = w / WPH;           // head within the group
+  const int head = g * GQA + j;
+  const int r0 = qt * BQ + (w % WPH) * 32;  // first query row of this wave
+  const int rq = r0 + n;
+  const bool q_ok = rq < q_len;
+  const int64_t q_tok = q_start + min(rq, q_len - 1);
+
+  __shared__ __attribute__((aligned(16))) u16 sK[kBK][kKStride];
+  __shared__ __attribute__((aligned(16))) u16 sVt[D][kVtStride];
+
+  // Q^T operand: lane holds dims 16kk + 8*hl + 0..7 of its query row, kk = 0..7.
+  bf16x8v qf[8];
+  {
+    const u16 *qp = a.q + q_tok * a.q_stride + (int64_t)head * D + 8 * hl;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = __builtin_bit_cast(bf16x8v, ld16(qp + 16 * kk));
+  }
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // Keys this workgroup needs: up to the last visible key of its last valid row.
+  const int kv_hi = min(kv_len, offset + min((qt + 1) * BQ, q_len));
+  const int n_tiles = ceil_div(kv_hi, kBK);
+  const int wave_last_key = offset + min(r0 + 31, q_len - 1);  // beyond: fully masked for this wave
+
+  // cooperative tile loads: K rows (t>>4)+16i, 16-byte chunk t&15; V row pair t&31, 16 dims (t>>5)
+  const int kr = tid >> 4, kc = tid & 15;
+  const int vp = tid & 31, vc = tid >> 5;
+  const int32_t *bt_row = PAGED ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
+  const int64_t cache_row = (int64_t)a.num_kv_heads * D;
+  const int bs_mask = (1 << a.bs_log2) - 1;
+
+  auto row_ptr = [&](const u16 *act, int64_t act_stride, const u16 *cache, int key) -> const u16 * {
+    if (PAGED) {
+      int blk = bt_row[key >> a.bs_log2];
+      blk = min(max(blk, 0), a.num_blocks - 1);
+      return cache + (((int64_t)blk << a.bs_log2) + (key & bs_mask)) * cache_row + (int64_t)g * D;
+    }
+    return act + (int64_t)(q_start + key) * act_stride + (int64_t)g * D;
+  };
+
+  u32x4 kreg[4], vreg[4];
+  auto load_tile = [&](int t) {
+    const int base = t * kBK;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = base + kr + 16 * i;
+      kreg[i] = key < kv_len ? ld16(row_ptr(a.k, a.k_stride, a.k_cache, key) + 8 * kc) : z;
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int key = base + 2 * vp + e;
+      const u16 *p = key < kv_len ? row_ptr(a.v, a.v_stride, a.v_cache, key) + 16 * vc : nullptr;
+      vreg[2 * e] = p ? ld16(p) : z;
+      vreg[2 * e + 1] = p ? ld16(p + 8) : z;
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(&sK[kr + 16 * i][8 * kc]) = kreg[i];
+    // transpose V: (V[2vp][d], V[2vp+1][d]) -> one dword of row d of V^T
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const u32 a0 = vreg[half][e], a1 = vreg[2 + half][e];
+        const int d = 16 * vc + 8 * half + 2 * e;
+        *reinterpret_cast<u32 *>(&sVt[d][2 * vp]) = pair_lo(a0, a1);
+        *reinterpret_cast<u32 *>(&sVt[d + 1][2 * vp]) = pair_hi(a0, a1);
+      }
+  };
+
+  if (n_tiles > 0) load_tile(0);
+  for (int t = 0; t < n_tiles; ++t) {
+    __syncthreads();  // previous tile fully consumed
+    store_tile();
+    __syncthreads();
+    if (t + 1 < n_tiles) load_tile(t + 1);
+    const int base = t * kBK;
+    if (r0 >= q_len || base > wave_last_key) continue;  // nothing visible to this wave in this tile
+
+    // S^T = K Q^T for keys base..base+63 (two 32-key blocks)
+    f32x16 st[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st[blk][i] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const bf16x8v kf = *reinterpret_cast<const bf16x8v *>(&sK[32 * blk + n][16 * kk + 8 * hl]);
+        st[blk] = mfma32(kf, qf[kk], st[blk]);
+      }
+    }
+    // scale + mask; key of register i of block blk: base + 32blk + 8(i/4) + 4hl + i%4
+    const bool need_mask = (base + kBK - 1 > offset + r0) || (base + kBK > kv_len);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float x = st[blk][i] * a.scale_log2e;
+        if (need_mask) {
+          const int key = base + 32 * blk + 8 * (i / 4) + 4 * hl + (i % 4);
+          if (key > offset + rq || key >= kv_len) x = -INFINITY;
+        }
+        st[blk][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - ref);
+    m_run = m_new;
+    float psum = 0.f;
+    bf16x8v pf[2][2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        u32x4 packed;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const u32 pr = pack_bf16x2(__builtin_amdgcn_exp2f(st[blk][8 * hh + 2 * e] - ref),
+                                     __builtin_amdgcn_exp2f(st[blk][8 * hh + 2 * e + 1] - ref));
+          psum += bf16_lo(pr) + bf16_hi(pr);
+          packed[e] = pr;
+        }
+        pf[blk][hh] = __builtin_bit_cast(bf16x8v, packed);
+      }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+
+    // O^T += V^T P^T; k-slot 8hl+e of step (blk, hh) is key 32blk + 16hh + 8(e/4) + 4hl + e%4
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int k0 = 32 * blk + 16 * hh + 4 * hl;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const u16 *vrow = &sVt[32 * db + n][0];
+          const u32x2 lo = *reinterpret_cast<const u32x2 *>(vrow + k0);
+          const u32x2 hi = *reinterpret_cast<const u32x2 *>(vrow + k0 + 8);
+          const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
+          acc[db] = mfma32(__builtin_bit_cast(bf16x8v, vv), pf[blk][hh], acc[db]);
+        }
+      }
+  }
+
+  // normalise and write: register i of block db is dim 32db + 8(i/4) + 4hl + i%4 of query column n
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (!q_ok) return;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  u16 *op = a.out + q_tok * a.out_stride + (int64_t)head * D + 4 * hl;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      u32x2 pk;
+      pk[0] = pack_bf16x2(acc[db][4 * i4] * inv, acc[db][4 * i4 + 1] * inv);
+      pk[1] = pack_bf16x2(acc[db][4 * i4 + 2] * inv, acc[db][4 * i4 + 3] * inv);
+      *reinterpret_cast<u32x2 *>(op + 32 * db + 8 * i4) = pk;
+    }
+}
+
+template <int GQA, bool PAGED>
+int launch(const PrefillArgs &a, int n_seqs, hipStream_t stream) {
+  dim3 grid(a.num_kv_heads, n_seqs, a.max_q_tiles);
+  hipLaunchKernelGGL((prefill_kernel<GQA, PAGED>), grid, dim3(256), 0, stream, a);
+  return launch_status();
+}
+
+template <bool PAGED>
+int dispatch(PrefillArgs a, int n_seqs, int gqa, int max_q_len, hipStream_t stream) {
+  switch (gqa) {
+    case 1: a.max_q_tiles = ceil_div(max_q_len, 128); return launch<1, PAGED>(a, n_seqs, stream);
+    case 2: a.max_q_tiles = ceil_div(max_q_len, 64); return launch<2, PAGED>(a, n_seqs, stream);
+    case 4: a.max_q_tiles = ceil_div(max_q_len, 32); return launch<4, PAGED>(a, n_seqs, stream);
+    default: return NVAMD_EUNSUPPORTED;
+  }
+}
+
+bool check_common(const void *out, int64_t out_stride, const void *q, int64_t q_stride, int num_heads,
+                  int num_kv_heads) {
+  return out && q && aligned16(out) && aligned16(q) && out_stride % 8 == 0 && q_stride % 8 == 0 &&
+         out_stride >= (int64_t)num_heads * kHeadDim && q_stride >= (int64_t)num_heads * kHeadDim &&
+         num_kv_heads > 0 && num_heads % num_kv_heads == 0;
+}
+
+}  // namespace
+}  // namespace nvamd
+
+using namespace nvamd;
+
+extern "C" int nvamd_varlen_prefill(void *out, int64_t out_stride, const void *q, int64_t q_stride, const void *k,
+                                    int64_t k_stride, const void *v, int64_t v_stride, const int32_t *cu_seqlens_q,
+                                    int n_seqs, int max_q_len, int num_heads, int num_kv_heads, int head_dim,
+                                    float scale, hipStream_t stream) {
+  if (n_seqs == 0 || max_q_len == 0) return NVAMD_OK;
+  if (head_dim != kHeadDim) return NVAMD_EUNSUPPORTED;
+  if (!check_common(out, out_stride, q, q_stride, num_heads, num_kv_heads) || !k || !v || !cu_seqlens_q ||
+      n_seqs < 0 || max_q_len < 0 || !aligned16(k) || !aligned16(v) || k_stride % 8 || v_stride % 8 ||
+      k_stride < (int64_t)num_kv_heads * head_dim || v_stride < (int64_t)num_kv_heads * head_dim || n_seqs > 65535)
+    return NVAMD_EINVAL;
+  PrefillArgs a = {};
+  a.out = static_cast<u16 *>(out);
+  a.out_stride = out_stride;
+  a.q = static_cast<const u16 *>(q);
+  a.q_stride = q_stride;
+  a.k = static_cast<const u16 *>(k);
+  a.k_stride = k_stride;
+  a.v = static_cast<const u16 *>(v);
+  a.v_stride = v_stride;
+  a.cu_seqlens_q = cu_seqlens_q;
+  a.num_kv_heads = num_kv_heads;
+  a.scale_log2e = scale * kLog2e;
+  return dispatch<false>(a, n_seqs, num_heads / num_kv_heads, max_q_len, stream);
+}
+
+extern "C" int nvamd_paged_prefill(void *out, int64_t out_stride, const void *q, int64_t q_stride,
+                                   const void *k_cache, const void *v_cache, int num_blocks, int block_size,
+                                   const int32_t *block_tables, int bt_stride, int bt_width,
+                                   const int32_t *cu_seqlens_q, const int32_t *kv_lens, int n_seqs, int max_q_len,
+                                   int num_heads, int num_kv_heads, int head_dim, float scale, hipStream_t stream) {
+  if (n_seqs == 0 || max_q_len == 0) return NVAMD_OK;
+  if (head_dim != kHeadDim) return NVAMD_EUNSUPPORTED;
+  const int bs_log2 = log2_exact(block_size);
+  if (bs_log2 < 0) return NVAMD_EUNSUPPORTED;
+  if (!check_common(out, out_stride, q, q_stride, num_heads, num_kv_heads) || !k_cache || !v_cache ||
+      !block_tables || !cu_seqlens_q || !kv_lens || n_seqs < 0 || max_q_len < 0 || num_blocks <= 0 ||
+      bt_width <= 0 || bt_stride < bt_width || !aligned16(k_cache) || !aligned16(v_cache) || n_seqs > 65535)
+    return NVAMD_EINVAL;
+  PrefillArgs a = {};
+  a.out = static_cast<u16 *>(out);
+  a.out_stride = out_stride;
+  a.q = static_cast<const u16 *>(q);
+  a.q_stride = q_stride;
+  a.k_cache = static_cast<const u16 *>(k_cache);
+  a.v_cache = static_cast<const u16 *>(v_cache);
+  a.block_tables = block_tables;
+  a.bt_stride = bt_stride;
+  a.bt_width = bt_width;
+  a.num_blocks = num_blocks;
+  a.bs_log2 = bs_log2;
+  a.cu_seqlens_q = cu_seqlens_q;
+  a.kv_lens = kv_lens;
+  a.num_kv_heads = num_kv_heads;
+  a.scale_log2e = scale * kLog2e;
+  return dispatch<true>(a, n_seqs, num_heads / num_kv_heads, max_q_len, stream);
+}
