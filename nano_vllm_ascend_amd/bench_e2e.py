@@ -1,0 +1,97 @@
+"""End-to-end throughput of continuous-batching generation (workload of examples/bench_compare.py:191-325).
+
+N requests of `input_len` random token ids (random.Random(seed), ids uniform
+in [0, min(10000, vocab-1)]) submitted as token ids, greedy decoding with EOS
+ignored for exactly `output_len` tokens each, one untimed warm-up run of the
+same workload, then `output_tok_s = total generated tokens / elapsed` over one
+timed run (prefill included).  The model is the Qwen3-0.6B shape with seeded
+random weights.
+
+    python -m nano_vllm_ascend_amd.bench_e2e --prompts 32 --input 256 --output 2048
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import random
+import time
+
+import torch
+
+from .config import QWEN3_0_6B
+from .engine import LLM
+from .sequence import Sequence
+
+
+def make_dataset(num_prompts: int, input_len: int, vocab_size: int, seed: int, token_id_high: int = 10000):
+    rng = random.Random(seed)
+    high = min(token_id_high, vocab_size - 1)
+    return [[rng.randint(0, high) for _ in range(input_len)] for _ in range(num_prompts)]
+
+
+def generate_from_token_ids(llm: LLM, prompts: list[list[int]], output_len: int, sampling_params=None):
+    """Submit token ids directly (no tokenizer), run to completion, return generated ids per request."""
+    from .sampling_params import SamplingParams
+
+    params = sampling_params or SamplingParams()
+    llm.scheduler.reset()
+    ids = []
+    for toks in prompts:
+        seq = Sequence(seq_id=llm.scheduler.next_seq_id(), prompt="", max_new_tokens=output_len,
+                       prompt_token_ids=torch.tensor(toks, dtype=torch.long), sampling_params=params)
+        llm.runner.prepare_sequences([seq])
+        seq.reserved_blocks = llm.scheduler.compute_required_blocks(runtime_prompt_len=seq.runtime_prompt_len,
+                                                                    max_new_tokens=output_len)
+        llm.scheduler.add_request(seq)
+        ids.append(seq.seq_id)
+    out = {}
+    while llm.has_unfinished():
+        for o in llm.step():
+            out[o["request_id"]] = o["token_ids"]
+    return [out.get(i, []) for i in ids]
+
+
+def run_e2e(num_prompts: int = 32, input_len: int = 256, output_len: int = 2048, seed: int = 0, device=None,
+            max_model_len: int = 4096, block_size: int = 128, warmup: int = 1, num_blocks: int | None = None,
+            enable_decode_graph: bool = True, llm: LLM | None = None) -> dict:
+    cfg = QWEN3_0_6B
+    need = num_prompts * -(-(input_len + output_len) // block_size)
+    if llm is None:
+        llm = LLM(cfg, max_model_len=max_model_len, block_size=block_size, num_blocks=num_blocks or need + 64,
+                  max_num_seqs=num_prompts, enable_decode_graph=enable_decode_graph, seed=seed)
+    llm.runner.tokenizer.eos_token_id = -1  # ignore EOS, as the reference benchmark does
+    prompts = make_dataset(num_prompts, input_len, cfg.vocab_size, seed)
+    for _ in range(warmup):
+        generate_from_token_ids(llm, prompts, output_len)
+        torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    outs = generate_from_token_ids(llm, prompts, output_len)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    generated = sum(len(o) for o in outs)
+    return {
+        "workload": f"{num_prompts}x{input_len}/{output_len} greedy ignore_eos",
+        "output_tok_s": round(generated / elapsed, 2),
+        "total_tok_s": round((generated + num_prompts * input_len) / elapsed, 2),
+        "elapsed_s": round(elapsed, 3),
+        "generated_tokens": generated,
+        "decode_graph": llm.runner.decode_graph_stats(),
+        "model": "Qwen3-0.6B shape, seeded N(0, 0.02) weights, bf16",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--prompts", type=int, default=32)
+    ap.add_argument("--input", type=int, default=256)
+    ap.add_argument("--output", type=int, default=2048)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    print(json.dumps(run_e2e(args.prompts, args.input, args.output, args.seed, warmup=args.warmup,
+                             enable_decode_graph=not args.no_graph)))
+
+
+if __name__ == "__main__":
+    main()

@@ -55,6 +55,9 @@ class PagedKVCacheMetadata:
     context_lens_host: list[int] = field(default_factory=list)
     max_context_len: int = 0
     max_query_len: int = 0
+    # decode: grid bound of the paged kernel (a captured graph fixes it) and its workspace
+    max_context_bound: int | None = None
+    decode_workspace: torch.Tensor | None = None
 
 
 @dataclass

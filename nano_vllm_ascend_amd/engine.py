@@ -89,6 +89,7 @@ class LLM:
             enable_decode_graph=enable_decode_graph,
             decode_graph_batch_sizes=decode_graph_batch_sizes,
             seed=seed,
+            max_num_seqs=max_num_seqs,
         )
         self.scheduler = MiniScheduler(
             max_num_seqs=max_num_seqs,

@@ -1,0 +1,206 @@
+"""Model runner: packing, graph/eager dispatch and sampling (nv/model_runner.py:15-297).
+
+Differences from the reference, all on the hot path:
+  - prefill and decode inputs (token ids, positions, slot_mapping, block
+    tables, context lengths, cu_seqlens, last-token indices) are packed on the
+    GPU from one host-to-device transfer per step (BlockManager._pack);
+  - decode at a captured batch size packs straight into the graph's static
+    buffers, so a replay needs no device-to-device input copies;
+  - greedy sampling of a batch is one argmax and ONE device-to-host read per
+    step (the reference synchronised once per sequence).
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from .block_manager import BlockManager
+from .config import load_config
+from .graph import DecodeGraphRunner
+from .layers import RotaryEmbedding, Sampler
+from .paged_kv_cache import PagedKVCache
+from .qwen3 import Qwen3ForCausalLM, load_safetensors_dir
+from .sequence import Sequence
+
+DEFAULT_DECODE_GRAPH_BATCH_SIZES = [1, 2, 4, 8, 16, 32]
+
+
+class TokenIdTokenizer:
+    """Stand-in when the model directory has no tokenizer: prompts must be token ids; decode gives ''."""
+
+    def __init__(self, eos_token_id: int):
+        self.eos_token_id = eos_token_id
+
+    def decode(self, token_ids, skip_special_tokens=True) -> str:
+        return ""
+
+
+def _load_tokenizer(model_path, eos_token_id: int):
+    if isinstance(model_path, (str, Path)) and Path(model_path).is_dir():
+        path = Path(model_path)
+        if (path / "tokenizer.json").exists() or (path / "tokenizer_config.json").exists():
+            from transformers import AutoTokenizer
+
+            return AutoTokenizer.from_pretrained(str(path), trust_remote_code=True, local_files_only=True)
+    return TokenIdTokenizer(eos_token_id)
+
+
+class ModelRunner:
+    def __init__(self, model_path, max_model_len: int, num_blocks: int | None, block_size: int, device_id: int,
+                 npu_memory_utilization: float, enable_prefix_cache: bool = False, enable_decode_graph: bool = False,
+                 decode_graph_batch_sizes: list[int] | None = None, seed: int = 0, max_num_seqs: int = 64):
+        torch.cuda.set_device(device_id)
+        self.device = torch.device("cuda", device_id)
+        self.model_path = model_path
+        self.max_model_len = max_model_len
+        self.block_size = block_size
+        self.dtype = torch.bfloat16
+        self.sampler = Sampler()
+        self.enable_prefix_cache = enable_prefix_cache
+        self.enable_decode_graph = enable_decode_graph
+        self.last_logits: torch.Tensor | None = None
+        self.config = load_config(model_path)
+        self.tokenizer = _load_tokenizer(model_path, self.config.eos_token_id)
+
+        self.model = self._load_model(seed)
+        self.num_blocks = num_blocks or self._num_blocks_from_memory(npu_memory_utilization)
+        self.block_manager = BlockManager(num_blocks=self.num_blocks, block_size=block_size, device=self.device,
+                                          max_seqs=max(max_num_seqs, 8),
+                                          max_blocks_per_seq=max(1, -(-max_model_len // block_size)))
+        cfg = self.config
+        self.kv_cache = PagedKVCache(cfg.num_hidden_layers, self.num_blocks, block_size, cfg.num_key_value_heads,
+                                     cfg.head_dim, self.dtype, self.device)
+        self.decode_graph_runner = None
+        if enable_decode_graph:
+            self.decode_graph_runner = DecodeGraphRunner(
+                model=self.model, kv_cache=self.kv_cache,
+                batch_sizes=decode_graph_batch_sizes or DEFAULT_DECODE_GRAPH_BATCH_SIZES,
+                max_model_len=max_model_len, block_size=block_size)
+
+    @torch.inference_mode()
+    def _load_model(self, seed: int) -> Qwen3ForCausalLM:
+        cfg = self.config
+        with torch.device(self.device):
+            model = Qwen3ForCausalLM(cfg, self.block_size, self.max_model_len)
+        model = model.to(dtype=self.dtype)
+        # the cast above rounded the RoPE table; rebuild it in fp32
+        model.model.rotary_emb = RotaryEmbedding(cfg.head_dim, cfg.max_position_embeddings,
+                                                 cfg.rope_theta).to(self.device)
+        sd = load_safetensors_dir(self.model_path) if isinstance(self.model_path, (str, Path)) else None
+        if sd is None:
+            model.init_random(seed)
+        else:
+            missing = model.load_hf_state_dict(sd)
+            if missing:
+                print(f"[load] missing={missing}")
+        model.eval()
+        return model
+
+    def _num_blocks_from_memory(self, utilization: float) -> int:
+        free, total = torch.cuda.mem_get_info(self.device)
+        budget = int(total * utilization) - (total - free)
+        cfg = self.config
+        per_block = PagedKVCache.bytes_per_block(cfg.num_hidden_layers, self.block_size, cfg.num_key_value_heads,
+                                                 cfg.head_dim)
+        return max(1, budget // per_block)
+
+    # -------------------------------------------------------------- prompts
+    def _tokenize_prompt(self, prompt) -> torch.Tensor:
+        if isinstance(prompt, str):
+            if isinstance(self.tokenizer, TokenIdTokenizer):
+                raise ValueError("this model directory has no tokenizer: submit prompts as token ids")
+            enc = self.tokenizer.apply_chat_template([{"role": "user", "content": prompt}],
+                                                     add_generation_prompt=True, enable_thinking=False,
+                                                     tokenize=True, return_dict=True, return_tensors="pt")
+            return enc["input_ids"][0]
+        return torch.as_tensor(prompt, dtype=torch.long).reshape(-1)
+
+    def tokenize_prompts(self, prompts) -> list[torch.Tensor]:
+        ids = [self._tokenize_prompt(p) for p in prompts]
+        longest = max(int(t.numel()) for t in ids)
+        if longest > self.max_model_len:
+            raise ValueError(f"prompt length {longest} exceeds max_model_len {self.max_model_len}")
+        return ids
+
+    def prepare_sequences(self, seqs: list[Sequence]) -> None:
+        """Prefix lookup at submit time (nv/model_runner.py:146-167)."""
+        bs = self.block_size
+        for seq in seqs:
+            seq.estimated_prompt_len = int(seq.prompt_token_ids.numel())
+            seq.cached_block_ids = []
+            seq.cached_prefix_len = 0
+            if self.enable_prefix_cache:
+                max_blocks = seq.estimated_prompt_len // bs
+                if seq.estimated_prompt_len % bs == 0 and max_blocks > 0:
+                    max_blocks -= 1
+                if max_blocks > 0:
+                    seq.cached_block_ids = self.block_manager.find_longest_prefix_blocks(
+                        seq.prompt_token_ids, max_cache_blocks=max_blocks)
+                    seq.cached_prefix_len = len(seq.cached_block_ids) * bs
+            seq.runtime_prompt_token_ids = seq.prompt_token_ids[seq.cached_prefix_len:]
+            seq.runtime_prompt_len = int(seq.runtime_prompt_token_ids.numel())
+            if seq.runtime_prompt_len <= 0:
+                raise ValueError(f"seq {seq.seq_id} has empty runtime prompt suffix")
+
+    # ------------------------------------------------------------ sampling
+    def _sample(self, logits: torch.Tensor, seqs: list[Sequence]) -> list[int]:
+        if all(seq.sampling_params.is_greedy() for seq in seqs):
+            return logits.argmax(dim=-1).tolist()  # one device-to-host read for the batch
+        return [int(self.sampler.sample(logits[i : i + 1], seq.sampling_params).item()) for i, seq in enumerate(seqs)]
+
+    # ------------------------------------------------------------- forward
+    @torch.inference_mode()
+    def prefill(self, seqs: list[Sequence]) -> None:
+        if not seqs:
+            return
+        md = self.block_manager.prepare_prefill_metadata(
+            slots=[s.seq_id for s in seqs], seq_lens=[s.runtime_prompt_len for s in seqs],
+            start_positions=[s.cached_prefix_len for s in seqs], prefix_block_ids=[s.cached_block_ids for s in seqs],
+            token_ids=[np.asarray(s.runtime_prompt_token_ids) for s in seqs])
+        out = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions, kv_cache=self.kv_cache,
+                         attn_metadata=md, is_prefill=True, logits_indices=md.last_token_indices)
+        self.last_logits = out.logits  # rows in `seqs` order; a graph replay reuses this buffer
+        for seq, token in zip(seqs, self._sample(out.logits, seqs)):
+            seq.set_prefill_result(next_token_id=token, prompt_len=seq.estimated_prompt_len)
+            if self.enable_prefix_cache:
+                self.block_manager.cache_full_blocks(slot=seq.seq_id, token_ids=seq.prompt_token_ids,
+                                                     num_cached_blocks=len(seq.cached_block_ids),
+                                                     num_full_blocks=seq.estimated_prompt_len // self.block_size)
+
+    @torch.inference_mode()
+    def decode(self, seqs: list[Sequence]) -> None:
+        if not seqs:
+            return
+        tokens = np.fromiter((seq.append_next_token() for seq in seqs), dtype=np.int64, count=len(seqs))
+        positions = [seq.cache_position for seq in seqs]
+        slots = [seq.seq_id for seq in seqs]
+        b = len(seqs)
+        logits = None
+        graph = self.decode_graph_runner
+        if graph is not None and graph.supports(b):
+            entry = graph.entry_for(b, 1, self.device, self.block_size)
+            md = self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens, width=entry.width,
+                                                            out=entry.buffers)
+            md = entry.metadata  # the static buffers now hold this step's inputs
+            logits = graph.replay(entry)
+        else:
+            if graph is not None:
+                graph.stats.fallbacks += 1
+            md = self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens)
+        if logits is None:
+            logits = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions, kv_cache=self.kv_cache,
+                                attn_metadata=md, is_prefill=False).logits
+        self.last_logits = logits
+        for seq, token in zip(seqs, self._sample(logits, seqs)):
+            seq.set_decode_result(token)
+
+    def decode_graph_stats(self) -> dict[str, int]:
+        return {} if self.decode_graph_runner is None else self.decode_graph_runner.stats_dict()
+
+    def free_seq(self, seq: Sequence) -> None:
+        self.block_manager.free_slot(seq.seq_id)
+
+    def clear_prefix_cache(self) -> None:
+        self.block_manager.clear_prefix_cache()

@@ -1,0 +1,183 @@
+"""Qwen3 decoder with the HIP attention path (nv/models/qwen3.py:1-221).
+
+Per layer: RMSNorm -> fused qkv projection -> qk_norm_rope (per-head RMSNorm,
+rotate-half RoPE and the KV store of post-RoPE k and raw v, one kernel) ->
+prefill or paged-decode attention -> o_proj -> residual -> RMSNorm -> SwiGLU
+MLP (fused gate/up projection) -> residual.  The projections are plain
+hipBLASLt GEMMs through torch; q/k/v are views into the fused projection
+output, which the kernels accept through their row strides.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .config import Qwen3Config
+from .layers import HipBatchPrefillAttention, HipPagedAttention, RMSNorm, RotaryEmbedding, qk_norm_rope
+
+
+@dataclass
+class CausalLMOutput:
+    logits: torch.Tensor
+
+
+class Qwen3Attention(nn.Module):
+    def __init__(self, config: Qwen3Config, layer_idx: int, block_size: int, max_model_len: int):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.num_heads = config.num_attention_heads
+        self.num_kv_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.qkv_weight = nn.Parameter(torch.empty(self.q_size + 2 * self.kv_size, config.hidden_size))
+        self.o_weight = nn.Parameter(torch.empty(config.hidden_size, self.q_size))
+        self.q_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+        self.k_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+        self.prefill_attn = HipBatchPrefillAttention(self.num_heads, self.num_kv_heads, self.head_dim, block_size,
+                                                     max_model_len)
+        self.paged_attn = HipPagedAttention(self.num_heads, self.num_kv_heads, self.head_dim)
+
+    def forward(self, hidden_states, rotary: RotaryEmbedding, positions, kv_cache, attn_metadata, is_prefill: bool):
+        t = hidden_states.shape[0]
+        qkv = F.linear(hidden_states, self.qkv_weight)
+        q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
+        k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
+        v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
+        qk_norm_rope(q, k, v, self.q_norm, self.k_norm, rotary, positions, kv_cache, self.layer_idx,
+                     attn_metadata.slot_mapping)
+        key_cache, value_cache = kv_cache.get_physical_cache(self.layer_idx)
+        if is_prefill:
+            attn = self.prefill_attn(q, k, v, attn_metadata, key_cache, value_cache)
+        else:
+            attn = self.paged_attn(q, key_cache, value_cache, attn_metadata.block_tables, attn_metadata.context_lens,
+                                   max_context_len=getattr(attn_metadata, "max_context_bound", None),
+                                   workspace=getattr(attn_metadata, "decode_workspace", None))
+        return F.linear(attn.reshape(t, self.q_size), self.o_weight)
+
+
+class Qwen3MLP(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.intermediate = config.intermediate_size
+        self.gate_up_weight = nn.Parameter(torch.empty(2 * config.intermediate_size, config.hidden_size))
+        self.down_weight = nn.Parameter(torch.empty(config.hidden_size, config.intermediate_size))
+
+    def forward(self, x):
+        gu = F.linear(x, self.gate_up_weight)
+        return F.linear(F.silu(gu[:, : self.intermediate]) * gu[:, self.intermediate :], self.down_weight)
+
+
+class Qwen3DecoderLayer(nn.Module):
+    def __init__(self, config: Qwen3Config, layer_idx: int, block_size: int, max_model_len: int):
+        super().__init__()
+        self.self_attn = Qwen3Attention(config, layer_idx, block_size, max_model_len)
+        self.mlp = Qwen3MLP(config)
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, h, rotary, positions, kv_cache, attn_metadata, is_prefill):
+        h = h + self.self_attn(self.input_layernorm(h), rotary, positions, kv_cache, attn_metadata, is_prefill)
+        return h + self.mlp(self.post_attention_layernorm(h))
+
+
+class Qwen3Model(nn.Module):
+    def __init__(self, config: Qwen3Config, block_size: int, max_model_len: int):
+        super().__init__()
+        self.embed_tokens = nn.Parameter(torch.empty(config.vocab_size, config.hidden_size))
+        self.layers = nn.ModuleList(
+            [Qwen3DecoderLayer(config, i, block_size, max_model_len) for i in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.rotary_emb = RotaryEmbedding(config.head_dim, config.max_position_embeddings, config.rope_theta)
+
+    def forward(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill):
+        h = F.embedding(input_ids_flat, self.embed_tokens)
+        for layer in self.layers:
+            h = layer(h, self.rotary_emb, position_ids_flat, kv_cache, attn_metadata, is_prefill)
+        return self.norm(h)
+
+
+class Qwen3ForCausalLM(nn.Module):
+    def __init__(self, config: Qwen3Config, block_size: int = 128, max_model_len: int = 2048):
+        super().__init__()
+        self.config = config
+        self.model = Qwen3Model(config, block_size, max_model_len)
+        self.lm_head = self.model.embed_tokens if config.tie_word_embeddings else nn.Parameter(
+            torch.empty(config.vocab_size, config.hidden_size))
+
+    def forward(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill: bool,
+                logits_indices=None) -> CausalLMOutput:
+        h = self.model(input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill)
+        if logits_indices is not None:
+            h = h.index_select(0, logits_indices)
+        return CausalLMOutput(logits=F.linear(h, self.lm_head))
+
+    # ---------------------------------------------------------------- weights
+    @torch.no_grad()
+    def init_random(self, seed: int = 0, std: float | None = None) -> None:
+        """Seeded N(0, std) for every projection and the embedding, ones for every norm weight."""
+        std = self.config.initializer_range if std is None else std
+        dev = self.model.embed_tokens.device
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        for name, p in self.named_parameters():
+            if name.endswith("norm.weight") or "layernorm" in name:
+                p.fill_(1.0)
+            else:
+                tmp = torch.empty(p.shape, dtype=torch.float32, device=dev)
+                tmp.normal_(0.0, std, generator=gen)
+                p.copy_(tmp)
+
+    @torch.no_grad()
+    def load_hf_state_dict(self, sd: dict) -> list[str]:
+        """Copy HF Qwen3ForCausalLM weights (q/k/v and gate/up are concatenated); returns missing names."""
+        missing = []
+        m = self.model
+
+        def put(dst, name):
+            if name in sd:
+                dst.copy_(sd[name])
+            else:
+                missing.append(name)
+
+        put(m.embed_tokens, "model.embed_tokens.weight")
+        put(m.norm.weight, "model.norm.weight")
+        for i, layer in enumerate(m.layers):
+            p = f"model.layers.{i}."
+            a = layer.self_attn
+            names = [p + "self_attn.q_proj.weight", p + "self_attn.k_proj.weight", p + "self_attn.v_proj.weight"]
+            if all(n in sd for n in names):
+                a.qkv_weight.copy_(torch.cat([sd[n] for n in names], 0))
+            else:
+                missing += [n for n in names if n not in sd]
+            put(a.o_weight, p + "self_attn.o_proj.weight")
+            put(a.q_norm.weight, p + "self_attn.q_norm.weight")
+            put(a.k_norm.weight, p + "self_attn.k_norm.weight")
+            names = [p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"]
+            if all(n in sd for n in names):
+                layer.mlp.gate_up_weight.copy_(torch.cat([sd[n] for n in names], 0))
+            else:
+                missing += [n for n in names if n not in sd]
+            put(layer.mlp.down_weight, p + "mlp.down_proj.weight")
+            put(layer.input_layernorm.weight, p + "input_layernorm.weight")
+            put(layer.post_attention_layernorm.weight, p + "post_attention_layernorm.weight")
+        if not self.config.tie_word_embeddings:
+            put(self.lm_head, "lm_head.weight")
+        return missing
+
+
+def load_safetensors_dir(path) -> dict | None:
+    """All tensors of the *.safetensors files in a local directory (safe loader; no pickle), or None."""
+    files = sorted(Path(path).glob("*.safetensors")) if Path(path).is_dir() else []
+    if not files:
+        return None
+    from safetensors.torch import load_file
+
+    sd = {}
+    for f in files:
+        sd.update(load_file(str(f)))
+    return sd
