@@ -45,7 +45,22 @@ def parse_args():
     ap.add_argument("--e2e-prompts", type=int, default=32)
     ap.add_argument("--e2e-input", type=int, default=256)
     ap.add_argument("--e2e-output", type=int, default=2048)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="only run 5 device copies of MB megabytes (calibrates HBM byte counters), then exit")
     return ap.parse_args()
+
+
+def copy_probe(mb: int) -> None:
+    """A plain device-to-device copy of known size: MB*2^20 bytes read and written per launch."""
+    import torch
+
+    n = mb * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "launches": 5}))
 
 
 def load_traffic(workload: str):
@@ -82,27 +97,25 @@ def decode_leg(args, device):
     layers = [(work.key_cache[l], work.value_cache[l]) for l in range(NUM_LAYERS)]
     stream = torch.cuda.current_stream()
 
-    def step(events=None):
-        for l, (kc, vc) in enumerate(layers):
+    def step():
+        for kc, vc in layers:
             _C.paged_decode(out, work.q, kc, vc, work.block_tables, work.context_lens, scale, max_ctx, ws)
-            if events is not None:
-                events.append(torch.cuda.Event(enable_timing=True))
-                events[-1].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # HIP events on the launch stream bracket the timed region; back-to-back launches of the
+    # same kernel, so region time / launches is the kernel's average launch duration
     start = torch.cuda.Event(enable_timing=True)
-    events: list = []
+    end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(args.steps):
-        step(events)
+        step()
+    end.record(stream)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(events[-1])
-    marks = [start] + events
-    launch_ms = [marks[i].elapsed_time(marks[i + 1]) for i in range(len(events))]
-    avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
+    total_ms = start.elapsed_time(end)
     launches = args.steps * NUM_LAYERS
+    avg_launch_s = total_ms / 1e3 / launches
     value = bytes_per_launch * launches / (total_ms / 1e3) / 1e9
     achieved = bytes_per_launch / avg_launch_s / 1e9
     return {
@@ -171,6 +184,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     device = torch.device("cuda:0")
     torch.manual_seed(args.seed)
 
