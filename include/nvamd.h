@@ -177,6 +177,29 @@ int nvamd_pack_batch(const int32_t *desc, int batch,
                      int64_t *last_token_indices, int64_t *input_ids,
                      hipStream_t stream);
 
+/* ------------------------------------------------------------------------- */
+/* Fused elementwise kernels of the decoder around the attention path.        */
+/* add_rms_norm: residual[r] += delta[r] (bf16 rounding; skipped when delta   */
+/*   is NULL), then out[r] = residual[r] * rsqrt(mean(residual[r]^2) + eps)   */
+/*   * weight, fp32 math, one bf16 rounding.  The decoder layer's residual    */
+/*   add + RMSNorm (nv/models/qwen3.py:138-150; npu_rms_norm at               */
+/*   nv/layers/layernorm.py:12-17).  hidden: a multiple of 1024, <= 4096.    */
+/* silu_mul: out[r, i] = bf16(bf16(silu(gu[r, i])) * gu[r, inter + i]) for the */
+/*   fused gate/up projection (nv/models/qwen3.py:34-35).                     */
+/* argmax_rows: out[r] = first index of the maximum of logits[r, 0:vocab]     */
+/*   (greedy sampling, torch.argmax at nv/layers/sampler.py:13-14).           */
+/* ------------------------------------------------------------------------- */
+int nvamd_add_rms_norm(const void *delta, void *residual, const void *weight,
+                       void *out, int rows, int hidden, float eps,
+                       hipStream_t stream);
+
+int nvamd_silu_mul(const void *gate_up, int64_t gu_stride, void *out,
+                   int64_t out_stride, int rows, int inter,
+                   hipStream_t stream);
+
+int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
+                      int vocab, int64_t *out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,9 @@ _SIGNATURES = {
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_ptr, _c_ptr,
          _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_ptr],
     ),
+    "nvamd_add_rms_norm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_float, _c_ptr]),
+    "nvamd_silu_mul": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
+    "nvamd_argmax_rows": (_c_int, [_c_ptr, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr]),
     "nvamd_qk_norm_rope": (
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr,
@@ -302,4 +305,47 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, v
         kv_lens.data_ptr(), n_seqs, int(max_q_len), q.shape[1], hkv, d, float(scale), _stream(),
     )
     _check(status, "nvamd_paged_prefill")
+    return out
+
+
+def add_rms_norm(delta: torch.Tensor | None, residual: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
+                 eps: float) -> torch.Tensor:
+    """residual += delta (if given); out = RMSNorm(residual) * weight.  Rows of 1024k bf16 elements."""
+    lib = load()
+    _bf16_cuda("residual", residual)
+    _bf16_cuda("out", out)
+    _require(residual.is_contiguous() and out.is_contiguous() and out.shape == residual.shape, "rows must be dense")
+    _require(weight.dtype == torch.bfloat16 and weight.numel() == residual.shape[-1], "weight must be bf16 [hidden]")
+    if delta is not None:
+        _require(delta.shape == residual.shape and delta.is_contiguous() and delta.dtype == torch.bfloat16,
+                 "delta must match residual")
+    hidden = residual.shape[-1]
+    status = lib.nvamd_add_rms_norm(_ptr(delta), residual.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                                    residual.numel() // hidden, hidden, float(eps), _stream())
+    _check(status, "nvamd_add_rms_norm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate_up[:, :I]) * gate_up[:, I:] for a [T, 2I] bf16 projection output."""
+    lib = load()
+    _bf16_cuda("gate_up", gate_up)
+    t, two_i = gate_up.shape
+    inter = two_i // 2
+    out = torch.empty((t, inter), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
+    status = lib.nvamd_silu_mul(gate_up.data_ptr(), _row_stride(gate_up), out.data_ptr(), _row_stride(out), t, inter,
+                                _stream())
+    _check(status, "nvamd_silu_mul")
+    return out
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """First index of each row's maximum (int64 [rows]) of a bf16 [rows, vocab] tensor."""
+    lib = load()
+    _bf16_cuda("logits", logits)
+    rows, vocab = logits.shape
+    out = torch.empty(rows, dtype=torch.int64, device=logits.device) if out is None else out
+    _require(out.dtype == torch.int64 and out.numel() >= rows, "out must be int64 [rows]")
+    status = lib.nvamd_argmax_rows(logits.data_ptr(), _row_stride(logits), rows, vocab, out.data_ptr(), _stream())
+    _check(status, "nvamd_argmax_rows")
     return out

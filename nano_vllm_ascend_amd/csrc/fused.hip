@@ -1,0 +1,181 @@
+// Fused elementwise kernels around the attention path (one launch each instead of
+// the chains of torch kernels the composite ops need):
+//   add_rms_norm  residual += delta (bf16);  out = RMSNorm(residual) * w
+//                 = the decoder layer's "h = residual + h; residual = h; h = norm(h)"
+//                 (nv/models/qwen3.py:138-150, npu_rms_norm at nv/layers/layernorm.py:12-17)
+//   silu_mul      out = silu(gate) * up on the fused [T, 2I] gate/up projection
+//                 (nv/models/qwen3.py:34-35)
+//   argmax_rows   greedy token of each logits row, first index on ties
+//                 (torch.argmax at nv/layers/sampler.py:13-14)
+// Rounding points match the reference's bf16 model: the residual sum is rounded
+// to bf16, the norm is computed in fp32 with one rounding, silu is rounded to
+// bf16 before the product, which is rounded again.
+#include "common.h"
+
+namespace nvamd {
+namespace {
+
+// One wave per row; lane l holds elements [16l, 16l+16) of each 1024-wide chunk.
+template <bool ADD>
+__global__ void __launch_bounds__(256)
+add_rms_norm_kernel(const u16 *__restrict__ delta, u16 *__restrict__ residual, const u16 *__restrict__ weight,
+                    u16 *__restrict__ out, int rows, int hidden, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t base = (int64_t)row * hidden;
+  constexpr int kMaxChunks = 4;  // hidden <= 4096
+  u32x4 v[kMaxChunks][2];
+  float ss = 0.f;
+  const int chunks = hidden / 1024;
+#pragma unroll
+  for (int ch = 0; ch < kMaxChunks; ++ch) {
+    if (ch >= chunks) break;
+    const int64_t off = base + ch * 1024 + 16 * lane;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 x = ld16(residual + off + 8 * h);
+      if (ADD) {
+        const u32x4 d = ld16(delta + off + 8 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          x[e] = pack_bf16x2(bf16_lo(x[e]) + bf16_lo(d[e]), bf16_hi(x[e]) + bf16_hi(d[e]));
+        st16(residual + off + 8 * h, x);
+      }
+      v[ch][h] = x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = bf16_lo(x[e]), b = bf16_hi(x[e]);
+        ss += a * a + b * b;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  const float rstd = rsqrtf(ss / (float)hidden + eps);
+#pragma unroll
+  for (int ch = 0; ch < kMaxChunks; ++ch) {
+    if (ch >= chunks) break;
+    const int64_t off = (int64_t)ch * 1024 + 16 * lane;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 w = ld16(weight + off + 8 * h);
+      u32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = pack_bf16x2(bf16_lo(v[ch][h][e]) * rstd * bf16_lo(w[e]), bf16_hi(v[ch][h][e]) * rstd * bf16_hi(w[e]));
+      st16(out + base + off + 8 * h, y);
+    }
+  }
+}
+
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+// One thread per 8 output elements.
+__global__ void __launch_bounds__(256)
+silu_mul_kernel(const u16 *__restrict__ gu, u16 *__restrict__ out, int rows, int inter, int64_t gu_stride,
+                int64_t out_stride) {
+  const int per_row = inter / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)rows * per_row) return;
+  const int r = (int)(i / per_row);
+  const int c = (int)(i % per_row) * 8;
+  const u32x4 g = ld16(gu + (int64_t)r * gu_stride + c);
+  const u32x4 u = ld16(gu + (int64_t)r * gu_stride + inter + c);
+  u32x4 y;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float s0 = round_bf16(silu_f32(bf16_lo(g[e])));
+    const float s1 = round_bf16(silu_f32(bf16_hi(g[e])));
+    y[e] = pack_bf16x2(s0 * bf16_lo(u[e]), s1 * bf16_hi(u[e]));
+  }
+  st16(out + (int64_t)r * out_stride + c, y);
+}
+
+// One workgroup per row: strided scan with 16-byte loads, then a (max, first index) reduction.
+__global__ void __launch_bounds__(256)
+argmax_rows_kernel(const u16 *__restrict__ logits, int64_t row_stride, int vocab, int64_t *__restrict__ out) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const u16 *p = logits + (int64_t)row * row_stride;
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+  const int vec_end = (vocab / 8) * 8;
+  for (int c = tid * 8; c < vec_end; c += 256 * 8) {
+    const u32x4 x = ld16(p + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = bf16_lo(x[e]), b = bf16_hi(x[e]);
+      if (a > best) { best = a; best_i = c + 2 * e; }
+      if (b > best) { best = b; best_i = c + 2 * e + 1; }
+    }
+  }
+  for (int c = vec_end + tid; c < vocab; c += 256) {
+    const float a = bf16_to_f32(p[c]);
+    if (a > best) { best = a; best_i = c; }
+  }
+  __shared__ float s_v[256];
+  __shared__ int s_i[256];
+  s_v[tid] = best;
+  s_i[tid] = best_i;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (tid < off) {
+      const float ov = s_v[tid + off];
+      const int oi = s_i[tid + off];
+      if (ov > s_v[tid] || (ov == s_v[tid] && oi < s_i[tid])) {
+        s_v[tid] = ov;
+        s_i[tid] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) out[row] = s_i[0] == 0x7fffffff ? 0 : s_i[0];
+}
+
+}  // namespace
+}  // namespace nvamd
+
+using namespace nvamd;
+
+extern "C" int nvamd_add_rms_norm(const void *delta, void *residual, const void *weight, void *out, int rows,
+                                  int hidden, float eps, hipStream_t stream) {
+  if (rows == 0) return NVAMD_OK;
+  if (!residual || !weight || !out || rows < 0) return NVAMD_EINVAL;
+  if (hidden % 1024 != 0 || hidden > 4096 || hidden <= 0) return NVAMD_EUNSUPPORTED;
+  if (!aligned16(residual) || !aligned16(weight) || !aligned16(out) || (delta && !aligned16(delta)))
+    return NVAMD_EINVAL;
+  const dim3 grid((rows + 3) / 4);
+  if (delta)
+    hipLaunchKernelGGL((add_rms_norm_kernel<true>), grid, dim3(256), 0, stream, static_cast<const u16 *>(delta),
+                       static_cast<u16 *>(residual), static_cast<const u16 *>(weight), static_cast<u16 *>(out), rows,
+                       hidden, eps);
+  else
+    hipLaunchKernelGGL((add_rms_norm_kernel<false>), grid, dim3(256), 0, stream, nullptr,
+                       static_cast<u16 *>(residual), static_cast<const u16 *>(weight), static_cast<u16 *>(out), rows,
+                       hidden, eps);
+  return launch_status();
+}
+
+extern "C" int nvamd_silu_mul(const void *gate_up, int64_t gu_stride, void *out, int64_t out_stride, int rows,
+                              int inter, hipStream_t stream) {
+  if (rows == 0) return NVAMD_OK;
+  if (!gate_up || !out || rows < 0 || inter <= 0 || inter % 8 || gu_stride < 2 * (int64_t)inter || gu_stride % 8 ||
+      out_stride < inter || out_stride % 8 || !aligned16(gate_up) || !aligned16(out))
+    return NVAMD_EINVAL;
+  const int64_t total = (int64_t)rows * (inter / 8);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return NVAMD_EINVAL;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, static_cast<const u16 *>(gate_up),
+                     static_cast<u16 *>(out), rows, inter, gu_stride, out_stride);
+  return launch_status();
+}
+
+extern "C" int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows, int vocab, int64_t *out,
+                                 hipStream_t stream) {
+  if (rows == 0) return NVAMD_OK;
+  if (!logits || !out || rows < 0 || vocab <= 0 || row_stride < vocab || row_stride % 8 || !aligned16(logits))
+    return NVAMD_EINVAL;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(256), 0, stream, static_cast<const u16 *>(logits),
+                     row_stride, vocab, out);
+  return launch_status();
+}

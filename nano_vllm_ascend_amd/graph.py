@@ -102,6 +102,7 @@ class DecodeGraphRunner:
             "slot_mapping": torch.zeros(b, dtype=torch.int64, device=device),
             "cu_seqlens_q": torch.zeros(b + 1, dtype=torch.int32, device=device),
             "last_token_indices": torch.zeros(b, dtype=torch.int64, device=device),
+            "greedy_ids": torch.zeros(b, dtype=torch.int64, device=device),  # in-graph argmax of the logits
         }
         cfg = getattr(self.model, "config", None)
         hq = getattr(cfg, "num_attention_heads", 1)
@@ -130,6 +131,8 @@ class DecodeGraphRunner:
             with self.graph_context(graph, self._pool):
                 out = self.model(input_ids_flat=b["input_ids"], position_ids_flat=b["positions"],
                                  kv_cache=self.kv_cache, attn_metadata=entry.metadata, is_prefill=False)
+                if getattr(out.logits, "is_cuda", False):
+                    _C.argmax_rows(out.logits, b["greedy_ids"])
             if self._pool is None and hasattr(graph, "pool"):
                 self._pool = graph.pool()
             entry.graph = graph

@@ -18,7 +18,11 @@ from . import _C
 
 
 class RMSNorm(nn.Module):
-    """x * rsqrt(mean(x^2) + eps) * w computed in fp32, one rounding to the input dtype (nv/layers/layernorm.py)."""
+    """x * rsqrt(mean(x^2) + eps) * w computed in fp32, one rounding to bf16 (nv/layers/layernorm.py).
+
+    ``forward`` runs the HIP add_rms_norm kernel without the add; ``add_forward``
+    fuses the decoder's residual add into the same launch.
+    """
 
     def __init__(self, hidden_size: int, eps: float = 1e-6):
         super().__init__()
@@ -26,9 +30,12 @@ class RMSNorm(nn.Module):
         self.variance_epsilon = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        var = xf.pow(2).mean(dim=-1, keepdim=True)
-        return (xf * torch.rsqrt(var + self.variance_epsilon) * self.weight.float()).to(x.dtype)
+        x = x.contiguous()
+        return _C.add_rms_norm(None, x, self.weight, torch.empty_like(x), self.variance_epsilon)
+
+    def add_forward(self, delta: torch.Tensor, residual: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """residual += delta in place; out = norm(residual)."""
+        return _C.add_rms_norm(delta, residual, self.weight, out, self.variance_epsilon)
 
 
 class RotaryEmbedding(nn.Module):

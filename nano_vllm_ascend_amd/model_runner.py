@@ -16,6 +16,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
+from . import _C
 from .block_manager import BlockManager
 from .config import load_config
 from .graph import DecodeGraphRunner
@@ -145,9 +146,10 @@ class ModelRunner:
                 raise ValueError(f"seq {seq.seq_id} has empty runtime prompt suffix")
 
     # ------------------------------------------------------------ sampling
-    def _sample(self, logits: torch.Tensor, seqs: list[Sequence]) -> list[int]:
+    def _sample(self, logits: torch.Tensor, seqs: list[Sequence], greedy_ids: torch.Tensor | None = None) -> list[int]:
         if all(seq.sampling_params.is_greedy() for seq in seqs):
-            return logits.argmax(dim=-1).tolist()  # one device-to-host read for the batch
+            ids = greedy_ids if greedy_ids is not None else _C.argmax_rows(logits)
+            return ids.tolist()  # one device-to-host read for the batch
         return [int(self.sampler.sample(logits[i : i + 1], seq.sampling_params).item()) for i, seq in enumerate(seqs)]
 
     # ------------------------------------------------------------- forward
@@ -178,6 +180,7 @@ class ModelRunner:
         slots = [seq.seq_id for seq in seqs]
         b = len(seqs)
         logits = None
+        greedy_ids = None
         graph = self.decode_graph_runner
         if graph is not None and graph.supports(b):
             entry = graph.entry_for(b, 1, self.device, self.block_size)
@@ -185,6 +188,8 @@ class ModelRunner:
                                                             out=entry.buffers)
             md = entry.metadata  # the static buffers now hold this step's inputs
             logits = graph.replay(entry)
+            if logits is not None:
+                greedy_ids = entry.buffers["greedy_ids"]
         else:
             if graph is not None:
                 graph.stats.fallbacks += 1
@@ -193,7 +198,7 @@ class ModelRunner:
             logits = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions, kv_cache=self.kv_cache,
                                 attn_metadata=md, is_prefill=False).logits
         self.last_logits = logits
-        for seq, token in zip(seqs, self._sample(logits, seqs)):
+        for seq, token in zip(seqs, self._sample(logits, seqs, greedy_ids)):
             seq.set_decode_result(token)
 
     def decode_graph_stats(self) -> dict[str, int]:

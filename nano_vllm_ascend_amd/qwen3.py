@@ -16,6 +16,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import _C
 from .config import Qwen3Config
 from .layers import HipBatchPrefillAttention, HipPagedAttention, RMSNorm, RotaryEmbedding, qk_norm_rope
 
@@ -68,8 +69,7 @@ class Qwen3MLP(nn.Module):
         self.down_weight = nn.Parameter(torch.empty(config.hidden_size, config.intermediate_size))
 
     def forward(self, x):
-        gu = F.linear(x, self.gate_up_weight)
-        return F.linear(F.silu(gu[:, : self.intermediate]) * gu[:, self.intermediate :], self.down_weight)
+        return F.linear(_C.silu_mul(F.linear(x, self.gate_up_weight)), self.down_weight)
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -95,10 +95,18 @@ class Qwen3Model(nn.Module):
         self.rotary_emb = RotaryEmbedding(config.head_dim, config.max_position_embeddings, config.rope_theta)
 
     def forward(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill):
-        h = F.embedding(input_ids_flat, self.embed_tokens)
-        for layer in self.layers:
-            h = layer(h, self.rotary_emb, position_ids_flat, kv_cache, attn_metadata, is_prefill)
-        return self.norm(h)
+        # The residual stream lives in one buffer updated in place; every "residual + h" and the
+        # RMSNorm that follows it is one add_rms_norm launch (same bf16 rounding as the reference).
+        residual = F.embedding(input_ids_flat, self.embed_tokens)
+        x = self.layers[0].input_layernorm(residual)
+        n = len(self.layers)
+        for i, layer in enumerate(self.layers):
+            a = layer.self_attn(x, self.rotary_emb, position_ids_flat, kv_cache, attn_metadata, is_prefill)
+            layer.post_attention_layernorm.add_forward(a, residual, x)
+            m = layer.mlp(x)
+            nxt = self.layers[i + 1].input_layernorm if i + 1 < n else self.norm
+            nxt.add_forward(m, residual, x)
+        return x
 
 
 class Qwen3ForCausalLM(nn.Module):
