@@ -89,6 +89,14 @@ __device__ __forceinline__ float wave_max_from_groups8(float v) {
   v = fmaxf(v, swizzle_xor16(v));
   return fmaxf(readlane(v, 0), readlane(v, 32));
 }
+// Full 64-lane maximum, wave-uniform result.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
 // Full 64-lane sum, wave-uniform result: reduce each 16-lane row, then add the 4 row sums.
 __device__ __forceinline__ float wave_sum(float v) {
   v = sum16(v);

@@ -2,13 +2,14 @@
 // nv/layers/npu_paged_attention.py:27-100).
 //
 // Work decomposition (split-KV, one kernel):
-//   grid = (num_kv_heads, batch, max_parts); a workgroup of NW waves owns one
-//   (sequence b, kv head g, partition p) of PART = NW * CPW * 64 consecutive
-//   context tokens, for all GQA query heads that read kv head g, so every K/V
-//   byte is read from HBM once.  Each wave owns CPW chunks of 64 tokens.
-//   The partition index is the slowest grid dimension, so workgroups are
-//   dispatched partition by partition and the empty ones that a loose context
-//   bound adds (graph capture uses max_model_len) come last.
+//   a workgroup of NW waves owns one (sequence b, kv head g, partition p) of
+//   PART = NW * CPW * 64 consecutive context tokens, for all GQA query heads
+//   that read kv head g, so every K/V byte is read from HBM once.  Each wave
+//   owns CPW chunks of 64 tokens.  The grid is 1-D over the items in b, g, p
+//   order with p fastest, counted over the partitions that exist for the
+//   device-side context lengths: a unit's partitions run side by side, so its
+//   merge overlaps other units' loads, and the slack a loose context bound adds
+//   (graph capture uses max_model_len) is a run of empty workgroups at the end.
 //
 // Lane layout inside a wave (64 lanes): r = lane/8 picks token rows r and r+8
 // of each 16-row tile, c = lane%8 picks dims 8c..8c+7 and 64+8c..64+8c+7.
@@ -25,10 +26,12 @@
 // GQA 2 fills 2 of 16 rows of an MFMA tile, so the contraction stays on v_dot2
 // in the vector ALUs, which have ample headroom: the kernel is HBM bound.
 //
-// Multi-partition sequences: every workgroup publishes (max, sum, acc[128])
-// per head with agent-scope write-through stores, waits for them, and bumps an
-// arrival counter; the last to arrive reads the partials with agent-scope loads
-// and writes the output.  No L2 writeback or invalidate is needed.
+// Merge: each wave folds its 8 row groups with DPP and swizzles, wave 0 folds the
+// NW waves through LDS.  A multi-partition unit's wave 0 then publishes
+// (max, sum, acc[128]) per head with agent-scope write-through stores, waits for
+// them, and bumps an arrival counter; the last to arrive reads every partial with
+// one round of agent-scope loads and writes the output.  No L2 writeback or
+// invalidate is needed.
 #include "common.h"
 
 namespace nvamd {
@@ -60,6 +63,7 @@ struct DecodeArgs {
   int bs_log2;
   int max_parts;
   int max_ctx;
+  int batch;
   float scale_log2e;
 };
 
@@ -69,44 +73,83 @@ struct KVTile {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ void store_agent(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float *p) {
-  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d);
+    if (lane >= d) v += t;
+  }
+  return v;
 }
 
+// Two adjacent floats (8-byte aligned) as one agent-scope 64-bit access.
+__device__ __forceinline__ void store_agent2(float *p, float lo, float hi) {
+  const uint64_t v = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void load_agent2(const float *p, float &lo, float &hi) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  lo = __uint_as_float((uint32_t)v);
+  hi = __uint_as_float((uint32_t)(v >> 32));
+}
+
+// GQA 1, and GQA 2 with one chunk per wave, fit 128 VGPRs without spills: four waves
+// per SIMD.
 template <int GQA, int NW, int CPW>
 __global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu((GQA == 1 || (GQA == 2 && CPW == 1)) ? 4 : 1)))
 paged_decode_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   constexpr int WT = CPW * 64;  // tokens per wave
   constexpr int PART = NW * WT;
 
-  const int g = blockIdx.x;
-  const int b = blockIdx.y;
-  const int p = blockIdx.z;
   const int hkv = a.num_kv_heads;
-
-  int ctx = a.context_lens[b];
-  ctx = min(ctx, min(a.max_ctx, a.bt_width << a.bs_log2));
-  ctx = max(ctx, 0);
-  const int n_parts = ceil_div(ctx, PART);
-  if (p >= (n_parts > 0 ? n_parts : 1)) return;
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+
+  // Work item of this workgroup: the blockIdx.x-th (b, g, p) in b, g, p order (p fastest)
+  // over the partitions that exist for the current context lengths; a sequence with no
+  // context has one item, which writes zeros.  Every wave finds it by itself: a wave-wide
+  // prefix sum of the partition counts, 64 sequences at a time.
+  const int ctx_cap = min(a.max_ctx, a.bt_width << a.bs_log2);
+  const int item = blockIdx.x;
+  int b = -1, n_parts = 0, first = 0, ctx = 0;
+  for (int b0 = 0, base = 0; b0 < a.batch; b0 += 64) {
+    const int bi = b0 + lane;
+    int ci = 0, np = 0;
+    if (bi < a.batch) {
+      ci = max(min(a.context_lens[bi], ctx_cap), 0);
+      np = max(ceil_div(ci, PART), 1);
+    }
+    const int incl = wave_incl_scan(np, lane);
+    const int total = __shfl(incl, 63);
+    if (item < (base + total) * hkv) {
+      const uint64_t past = __ballot((base + incl) * hkv > item);
+      const int sel = __ffsll((unsigned long long)past) - 1;
+      b = b0 + sel;
+      n_parts = __shfl(np, sel);
+      first = base + __shfl(incl, sel) - n_parts;
+      ctx = __shfl(ci, sel);
+      break;
+    }
+    base += total;
+  }
+  if (b < 0) return;  // past the last item
+  b = __builtin_amdgcn_readfirstlane(b);
+  n_parts = __builtin_amdgcn_readfirstlane(n_parts);
+  ctx = __builtin_amdgcn_readfirstlane(ctx);
+  const int rem = item - __builtin_amdgcn_readfirstlane(first) * hkv;
+  const int g = rem / n_parts;
+  const int p = rem - g * n_parts;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int r = lane >> 3;
   const int c = lane & 7;
 
-  __shared__ float s_o[NW][GQA][8][D];
-  __shared__ float s_l[NW][GQA][8];
-  __shared__ float s_m[NW][GQA][8];
-  __shared__ float s_f[NW][GQA][8];
-  __shared__ float s_pm[64][GQA];  // merge stage: per-partition factors
-  __shared__ float s_pl[GQA];
-  __shared__ int s_last;
+  __shared__ float s_o[NW][2][GQA][D];  // per wave and half-wave: summed row groups
+  __shared__ float s_l[NW][2][GQA];
+  __shared__ float s_m[NW][GQA];
 
   // Query rows of the GQA group, as bf16 pairs for v_dot2.
   u32x4 qr[GQA][2];
@@ -242,108 +285,128 @@ paged_decode_kernel(DecodeArgs a) {
     }
   }
 
-  // Workgroup merge of the NW * 8 row-group states of each head.
+  // Wave merge: rescale the 8 row groups to the wave-wide max, then add groups r and r^1
+  // (DPP row_ror:8) and r and r^2 (swizzle xor 16).  Lanes 0-31 then hold the sum over
+  // groups 0-3 and lanes 32-63 the sum over groups 4-7.
+  const int half = lane >> 5;
 #pragma unroll
   for (int j = 0; j < GQA; ++j) {
-    float *dst = &s_o[w][j][r][0];
-    // o[j][0..7] hold dims 8c..8c+7, o[j][8..15] hold dims 64+8c..64+8c+7
-    *reinterpret_cast<f32x4 *>(dst + 8 * c) = f32x4{o[j][0], o[j][1], o[j][2], o[j][3]};
-    *reinterpret_cast<f32x4 *>(dst + 8 * c + 4) = f32x4{o[j][4], o[j][5], o[j][6], o[j][7]};
-    *reinterpret_cast<f32x4 *>(dst + 64 + 8 * c) = f32x4{o[j][8], o[j][9], o[j][10], o[j][11]};
-    *reinterpret_cast<f32x4 *>(dst + 64 + 8 * c + 4) = f32x4{o[j][12], o[j][13], o[j][14], o[j][15]};
-    if (c == 0) {
-      s_l[w][j][r] = l[j];
-      s_m[w][j][r] = m[j];
+    const float M = wave_max_from_groups8(m[j]);
+    const float f = m[j] == -INFINITY ? 0.f : fast_exp2(m[j] - M);
+    float lj = l[j] * f;
+    lj += dpp<kDppRowRor8>(lj);
+    lj += swizzle_xor16(lj);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float v = o[j][e] * f;
+      v += dpp<kDppRowRor8>(v);
+      v += swizzle_xor16(v);
+      o[j][e] = v;
     }
+    if ((lane & 31) < 8) {  // lanes 0-7 and 32-39 publish their half
+      float *dst = &s_o[w][half][j][0];
+      *reinterpret_cast<f32x4 *>(dst + 8 * c) = f32x4{o[j][0], o[j][1], o[j][2], o[j][3]};
+      *reinterpret_cast<f32x4 *>(dst + 8 * c + 4) = f32x4{o[j][4], o[j][5], o[j][6], o[j][7]};
+      *reinterpret_cast<f32x4 *>(dst + 64 + 8 * c) = f32x4{o[j][8], o[j][9], o[j][10], o[j][11]};
+      *reinterpret_cast<f32x4 *>(dst + 64 + 8 * c + 4) = f32x4{o[j][12], o[j][13], o[j][14], o[j][15]};
+      if (c == 0) s_l[w][half][j] = lj;
+    }
+    if (lane == 0) s_m[w][j] = M;
   }
   __syncthreads();
-  if (tid < NW * GQA * 8) {
-    const int ww = tid / (GQA * 8);
-    const int j = (tid / 8) % GQA;
-    const int rr = tid % 8;
-    float M = -INFINITY;
-    for (int x = 0; x < NW; ++x)
-      for (int y = 0; y < 8; ++y) M = fmaxf(M, s_m[x][j][y]);
-    const float mv = s_m[ww][j][rr];
-    s_f[ww][j][rr] = mv == -INFINITY ? 0.f : fast_exp2(mv - M);
-    if (ww == 0 && rr == 0) s_pl[j] = M;
-  }
-  __syncthreads();
+  if (w != 0) return;  // wave 0 finishes the workgroup
 
+  // Workgroup merge: lane owns dims 2*lane, 2*lane+1 of every head.
+  float acc[GQA][2], ls[GQA], mx[GQA];
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int x = 0; x < NW; ++x) M = fmaxf(M, s_m[x][j]);
+    acc[j][0] = acc[j][1] = ls[j] = 0.f;
+#pragma unroll
+    for (int x = 0; x < NW; ++x) {
+      const float mv = s_m[x][j];
+      const float f = mv == -INFINITY ? 0.f : fast_exp2(mv - M);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float2 ov = *reinterpret_cast<const float2 *>(&s_o[x][h][j][2 * lane]);
+        acc[j][0] += f * ov.x;
+        acc[j][1] += f * ov.y;
+        ls[j] += f * s_l[x][h][j];
+      }
+    }
+    mx[j] = M;
+  }
+
+  u16 *out_base = a.out + (int64_t)b * a.out_stride + (int64_t)g * GQA * D + 2 * lane;
+  if (n_parts <= 1) {
+#pragma unroll
+    for (int j = 0; j < GQA; ++j) {
+      const float inv = ls[j] > 0.f ? 1.f / ls[j] : 0.f;
+      *reinterpret_cast<u32 *>(out_base + j * D) = pack_bf16x2(acc[j][0] * inv, acc[j][1] * inv);
+    }
+    return;
+  }
+
+  // Publish (max, sum, acc[128]) per head with write-through stores, wait for them, then
+  // count the arrival.  The last wave 0 of (b, g) to arrive merges all partitions.
   float *part_base = a.partials + (((int64_t)b * hkv + g) * a.max_parts) * GQA * kPartFloats;
-  u16 *out_base = a.out + (int64_t)b * a.out_stride + (int64_t)g * GQA * D;
-
-  for (int idx = tid; idx < GQA * D; idx += NW * 64) {
-    const int j = idx / D;
-    const int d = idx % D;
-    float acc = 0.f, ls = 0.f;
 #pragma unroll
-    for (int x = 0; x < NW; ++x)
-#pragma unroll
-      for (int y = 0; y < 8; ++y) {
-        const float f = s_f[x][j][y];
-        acc += f * s_o[x][j][y][d];
-        ls += f * s_l[x][j][y];
-      }
-    if (n_parts <= 1) {
-      out_base[j * D + d] = f32_to_bf16(ls > 0.f ? acc / ls : 0.f);
-    } else {
-      float *pr = part_base + ((int64_t)p * GQA + j) * kPartFloats;
-      store_agent(pr + 2 + d, acc);
-      if (d == 0) {
-        store_agent(pr, s_pl[j]);
-        store_agent(pr + 1, ls);
-      }
-    }
+  for (int j = 0; j < GQA; ++j) {
+    float *pr = part_base + ((int64_t)p * GQA + j) * kPartFloats;
+    store_agent2(pr + 2 + 2 * lane, acc[j][0], acc[j][1]);
+    if (lane == 0) store_agent2(pr, mx[j], ls[j]);
   }
-  if (n_parts <= 1) return;
-
-  // Publish: wait until this workgroup's write-through stores are complete,
-  // then count the arrival.  The last workgroup of (b, g) merges.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keep the stores above the wait
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // keep the stores above the wait
   __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
   int *counter = a.counters + (int64_t)b * hkv + g;
-  if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == n_parts - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
+  int prev = 0;
+  if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0);
+  if (prev != n_parts - 1) return;
 
-  if (tid < n_parts * GQA) {
-    const int pp2 = tid / GQA;
-    const int j = tid % GQA;
-    const float *pr = part_base + ((int64_t)pp2 * GQA + j) * kPartFloats;
-    s_pm[pp2][j] = load_agent(pr);
+  // Merge.  Lane x holds partition x's (max, sum) of every head (one round of loads),
+  // then the accumulators arrive 8 partitions per round, all loads issued before use.
+  float fx[GQA], den[GQA];
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) {
+    float pm = -INFINITY, pl = 0.f;
+    if (lane < n_parts) load_agent2(part_base + ((int64_t)lane * GQA + j) * kPartFloats, pm, pl);
+    const float M = wave_max(pm);
+    fx[j] = pm == -INFINITY ? 0.f : fast_exp2(pm - M);
+    den[j] = wave_sum(fx[j] * pl);
   }
-  __syncthreads();
-  if (tid < GQA) {
-    float M = -INFINITY;
-    for (int x = 0; x < n_parts; ++x) M = fmaxf(M, s_pm[x][tid]);
-    s_pl[tid] = M;
-  }
-  __syncthreads();
-  if (tid < n_parts * GQA) {
-    const int pp2 = tid / GQA;
-    const int j = tid % GQA;
-    const float mp = s_pm[pp2][j];
-    s_pm[pp2][j] = mp == -INFINITY ? 0.f : fast_exp2(mp - s_pl[j]);
-  }
-  __syncthreads();
-  for (int idx = tid; idx < GQA * D; idx += NW * 64) {
-    const int j = idx / D;
-    const int d = idx % D;
-    float num = 0.f, den = 0.f;
-    for (int x = 0; x < n_parts; ++x) {
-      const float *pr = part_base + ((int64_t)x * GQA + j) * kPartFloats;
-      const float f = s_pm[x][j];
-      num += f * load_agent(pr + 2 + d);
-      den += f * load_agent(pr + 1);
+  float n0[GQA], n1[GQA];
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) n0[j] = n1[j] = 0.f;
+  for (int x0 = 0; x0 < n_parts; x0 += 8) {
+    float v0[GQA][8], v1[GQA][8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int x = min(x0 + k, n_parts - 1);
+#pragma unroll
+      for (int j = 0; j < GQA; ++j)
+        load_agent2(part_base + ((int64_t)x * GQA + j) * kPartFloats + 2 + 2 * lane, v0[j][k], v1[j][k]);
     }
-    out_base[j * D + d] = f32_to_bf16(den > 0.f ? num / den : 0.f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (x0 + k < n_parts) {
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+          const float f = readlane(fx[j], x0 + k);
+          n0[j] += f * v0[j][k];
+          n1[j] += f * v1[j][k];
+        }
+      }
+    }
   }
-  if (tid == 0) {  // leave the workspace ready for the next call
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) {
+    const float inv = den[j] > 0.f ? 1.f / den[j] : 0.f;
+    *reinterpret_cast<u32 *>(out_base + j * D) = pack_bf16x2(n0[j] * inv, n1[j] * inv);
+  }
+  if (lane == 0) {  // leave the workspace ready for the next call
     __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -353,7 +416,9 @@ int launch(DecodeArgs a, int batch, hipStream_t stream) {
   constexpr int PART = NW * CPW * 64;
   a.max_parts = ceil_div(a.max_ctx, PART);
   if (a.max_parts > 64) return NVAMD_EUNSUPPORTED;  // merge stage holds <= 64 partitions
-  dim3 grid(a.num_kv_heads, batch, a.max_parts);
+  a.batch = batch;
+  // One workgroup per possible (b, g, p); the ones past the last existing item exit at once.
+  dim3 grid((unsigned)((int64_t)batch * a.num_kv_heads * a.max_parts));
   hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW>), grid, dim3(NW * 64), 0, stream, a);
   return launch_status();
 }
@@ -409,6 +474,7 @@ extern "C" int nvamd_paged_decode(void *out, int64_t out_stride, const void *q, 
   if ((int64_t)batch * num_kv_heads > kCounterSlots || batch > 65535) return NVAMD_EUNSUPPORTED;
   const size_t need = nvamd_paged_decode_workspace_size(batch, num_heads, num_kv_heads, max_context_len);
   if (!workspace || workspace_bytes < need) return NVAMD_EWORKSPACE;
+  if (!aligned16(workspace)) return NVAMD_EINVAL;
 
   DecodeArgs a;
   a.out = static_cast<u16 *>(out);

@@ -55,6 +55,25 @@ def test_decode_edge_lengths(device, ctx):
 
 
 @pytest.mark.gpu
+def test_decode_large_ragged_batch_with_empty_sequences(device):
+    """150 sequences (the work list spans three 64-sequence scans), some with no context."""
+    gen = torch.Generator().manual_seed(21)
+    ctx = torch.randint(0, 1500, (150,), generator=gen).tolist()
+    for i in (0, 63, 64, 100, 149):
+        ctx[i] = 0
+    ctx[1], ctx[65] = 1, 1499
+    work = W.make_decode(150, 0, 0, 1400, seed=21, device=device, context_lens=ctx)
+    out_tight = run_decode(work.q, work.key_cache[0], work.value_cache[0], work.block_tables, work.context_lens,
+                           max(ctx))
+    check(work, max_ctx=4096)
+    torch.cuda.synchronize()
+    assert int(out_tight[[0, 63, 64, 100, 149]].abs().sum()) == 0  # empty sequences give zeros
+    ref = paged_decode_ref(work.q, work.key_cache[0], work.value_cache[0], work.block_tables, work.context_lens,
+                           SCALE)
+    assert (out_tight.float().cpu() - ref).abs().max().item() <= TOL
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("heads", [(8, 8), (16, 8), (16, 4)])
 def test_decode_gqa_groups(device, heads):
     hq, hkv = heads
