@@ -200,6 +200,28 @@ int nvamd_silu_mul(const void *gate_up, int64_t gu_stride, void *out,
 int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
                       int vocab, int64_t *out, hipStream_t stream);
 
+/* ------------------------------------------------------------------------- */
+/* Skinny-M projections of the decode step (M <= 32 rows), a weight stream:   */
+/* linear: y[m, n] = bf16(sum_k x[m, k] * w[n, k]), fp32 accumulation.  The   */
+/*   decoder's qkv / o / down projections and the LM head at decode batch     */
+/*   sizes (F.linear at nv/models/qwen3.py:26-35, 48-51, 119 and              */
+/*   nv/layers/embed_head.py:24-39).  n % 32 == 0, k % 256 == 0, x and w      */
+/*   16-byte aligned with row strides (elements) that are multiples of 8.     */
+/* linear_silu_mul: y[m, i] = bf16(bf16(silu(g)) * u), g = bf16(x . w[i]),    */
+/*   u = bf16(x . w[inter + i]) over the fused [2 * inter, k] gate/up weight  */
+/*   (nv/models/qwen3.py:34-35): the gate/up projection and silu_mul in one   */
+/*   launch, with the same rounding points.  inter % 32 == 0.                 */
+/* Both return NVAMD_EUNSUPPORTED for m > 32 (use a library GEMM there).       */
+/* ------------------------------------------------------------------------- */
+int nvamd_linear(const void *x, int64_t x_stride, const void *w,
+                 int64_t w_stride, void *y, int64_t y_stride, int m, int n,
+                 int k, hipStream_t stream);
+
+int nvamd_linear_silu_mul(const void *x, int64_t x_stride,
+                          const void *w_gate_up, int64_t w_stride, void *y,
+                          int64_t y_stride, int m, int inter, int k,
+                          hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

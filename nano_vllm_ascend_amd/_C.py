@@ -56,6 +56,9 @@ _SIGNATURES = {
     "nvamd_add_rms_norm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_float, _c_ptr]),
     "nvamd_silu_mul": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
     "nvamd_argmax_rows": (_c_int, [_c_ptr, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr]),
+    "nvamd_linear": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_int, _c_ptr]),
+    "nvamd_linear_silu_mul": (
+        _c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_int, _c_ptr]),
     "nvamd_qk_norm_rope": (
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr,
@@ -348,4 +351,41 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     _require(out.dtype == torch.int64 and out.numel() >= rows, "out must be int64 [rows]")
     status = lib.nvamd_argmax_rows(logits.data_ptr(), _row_stride(logits), rows, vocab, out.data_ptr(), _stream())
     _check(status, "nvamd_argmax_rows")
+    return out
+
+
+SKINNY_MAX_ROWS = 32  # rows the skinny projection kernels take (decode batches)
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x[M, K] @ w[N, K]^T in bf16 for M <= 32 (HIP skinny GEMM)."""
+    lib = load()
+    _bf16_cuda("x", x)
+    _bf16_cuda("w", w)
+    m, k = x.shape
+    n = w.shape[0]
+    _require(w.shape[1] == k, "w must be [N, K]")
+    out = torch.empty((m, n), dtype=x.dtype, device=x.device) if out is None else out
+    _require(out.shape == (m, n) and out.dtype == torch.bfloat16 and out.stride(1) == 1, "out must be bf16 [M, N]")
+    status = lib.nvamd_linear(x.data_ptr(), _row_stride(x), w.data_ptr(), _row_stride(w), out.data_ptr(),
+                              out.stride(0), m, n, k, _stream())
+    _check(status, "nvamd_linear")
+    return out
+
+
+def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(x @ w_gate_up[:I]^T) * (x @ w_gate_up[I:]^T) in bf16 for M <= 32 (one HIP launch)."""
+    lib = load()
+    _bf16_cuda("x", x)
+    _bf16_cuda("w_gate_up", w_gate_up)
+    m, k = x.shape
+    two_i = w_gate_up.shape[0]
+    _require(w_gate_up.shape[1] == k and two_i % 2 == 0, "w_gate_up must be [2I, K]")
+    inter = two_i // 2
+    out = torch.empty((m, inter), dtype=x.dtype, device=x.device) if out is None else out
+    _require(out.shape == (m, inter) and out.dtype == torch.bfloat16 and out.stride(1) == 1,
+             "out must be bf16 [M, I]")
+    status = lib.nvamd_linear_silu_mul(x.data_ptr(), _row_stride(x), w_gate_up.data_ptr(), _row_stride(w_gate_up),
+                                       out.data_ptr(), out.stride(0), m, inter, k, _stream())
+    _check(status, "nvamd_linear_silu_mul")
     return out

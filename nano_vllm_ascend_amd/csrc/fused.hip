@@ -91,45 +91,65 @@ silu_mul_kernel(const u16 *__restrict__ gu, u16 *__restrict__ out, int rows, int
   st16(out + (int64_t)r * out_stride + c, y);
 }
 
-// One workgroup per row: strided scan with 16-byte loads, then a (max, first index) reduction.
-__global__ void __launch_bounds__(256)
+// (value, index) order of greedy sampling: larger value first, then the smaller index.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+// One 1024-thread workgroup per row.  A thread scans 16-byte vectors in increasing index
+// order, four loads in flight per step, keeping the first index of its maximum; waves then
+// reduce with shuffles and the 16 wave results meet in LDS.
+constexpr int kArgmaxThreads = 1024;
+__global__ void __launch_bounds__(kArgmaxThreads)
 argmax_rows_kernel(const u16 *__restrict__ logits, int64_t row_stride, int vocab, int64_t *__restrict__ out) {
+  constexpr int U = 4;
+  constexpr int kStep = kArgmaxThreads * 8;
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const u16 *p = logits + (int64_t)row * row_stride;
   float best = -INFINITY;
   int best_i = 0x7fffffff;
   const int vec_end = (vocab / 8) * 8;
-  for (int c = tid * 8; c < vec_end; c += 256 * 8) {
-    const u32x4 x = ld16(p + c);
+  for (int c0 = tid * 8; c0 < vec_end; c0 += U * kStep) {
+    u32x4 x[U];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float a = bf16_lo(x[e]), b = bf16_hi(x[e]);
-      if (a > best) { best = a; best_i = c + 2 * e; }
-      if (b > best) { best = b; best_i = c + 2 * e + 1; }
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * kStep;
+      x[u] = c < vec_end ? ld16(p + c) : u32x4{0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u};  // -inf
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = c0 + u * kStep + 2 * e;
+        const float a = bf16_lo(x[u][e]), b = bf16_hi(x[u][e]);
+        if (a > best) { best = a; best_i = c; }
+        if (b > best) { best = b; best_i = c + 1; }
+      }
   }
-  for (int c = vec_end + tid; c < vocab; c += 256) {
+  for (int c = vec_end + tid; c < vocab; c += kArgmaxThreads) {
     const float a = bf16_to_f32(p[c]);
     if (a > best) { best = a; best_i = c; }
   }
-  __shared__ float s_v[256];
-  __shared__ int s_i[256];
-  s_v[tid] = best;
-  s_i[tid] = best_i;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (tid < off) {
-      const float ov = s_v[tid + off];
-      const int oi = s_i[tid + off];
-      if (ov > s_v[tid] || (ov == s_v[tid] && oi < s_i[tid])) {
-        s_v[tid] = ov;
-        s_i[tid] = oi;
-      }
-    }
-    __syncthreads();
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int oi = __shfl_xor(best_i, off);
+    if (better(ov, oi, best, best_i)) { best = ov; best_i = oi; }
   }
-  if (tid == 0) out[row] = s_i[0] == 0x7fffffff ? 0 : s_i[0];
+  __shared__ float s_v[kArgmaxThreads / 64];
+  __shared__ int s_i[kArgmaxThreads / 64];
+  const int w = tid >> 6;
+  if ((tid & 63) == 0) {
+    s_v[w] = best;
+    s_i[w] = best_i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float bv = s_v[0];
+    int bi = s_i[0];
+    for (int x = 1; x < kArgmaxThreads / 64; ++x)
+      if (better(s_v[x], s_i[x], bv, bi)) { bv = s_v[x]; bi = s_i[x]; }
+    out[row] = bi == 0x7fffffff ? 0 : bi;
+  }
 }
 
 }  // namespace
@@ -175,7 +195,7 @@ extern "C" int nvamd_argmax_rows(const void *logits, int64_t row_stride, int row
   if (rows == 0) return NVAMD_OK;
   if (!logits || !out || rows < 0 || vocab <= 0 || row_stride < vocab || row_stride % 8 || !aligned16(logits))
     return NVAMD_EINVAL;
-  hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(256), 0, stream, static_cast<const u16 *>(logits),
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(kArgmaxThreads), 0, stream, static_cast<const u16 *>(logits),
                      row_stride, vocab, out);
   return launch_status();
 }

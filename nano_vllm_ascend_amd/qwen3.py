@@ -3,9 +3,11 @@
 Per layer: RMSNorm -> fused qkv projection -> qk_norm_rope (per-head RMSNorm,
 rotate-half RoPE and the KV store of post-RoPE k and raw v, one kernel) ->
 prefill or paged-decode attention -> o_proj -> residual -> RMSNorm -> SwiGLU
-MLP (fused gate/up projection) -> residual.  The projections are plain
-hipBLASLt GEMMs through torch; q/k/v are views into the fused projection
-output, which the kernels accept through their row strides.
+MLP (fused gate/up projection) -> residual.  q/k/v are views into the fused projection
+output, which the kernels accept through their row strides.  At decode batch sizes
+(<= 32 rows) the qkv projection and the gate/up projection + SiLU*mul run on the
+skinny-M HIP GEMM (the latter as one launch); the o/down projections and the LM head
+stay on hipBLASLt, which is faster for their shapes.
 """
 from __future__ import annotations
 
@@ -18,7 +20,8 @@ from torch import nn
 
 from . import _C
 from .config import Qwen3Config
-from .layers import HipBatchPrefillAttention, HipPagedAttention, RMSNorm, RotaryEmbedding, qk_norm_rope
+from .layers import (HipBatchPrefillAttention, HipPagedAttention, RMSNorm, RotaryEmbedding, gate_up_silu, linear,
+                     qk_norm_rope)
 
 
 @dataclass
@@ -45,7 +48,7 @@ class Qwen3Attention(nn.Module):
 
     def forward(self, hidden_states, rotary: RotaryEmbedding, positions, kv_cache, attn_metadata, is_prefill: bool):
         t = hidden_states.shape[0]
-        qkv = F.linear(hidden_states, self.qkv_weight)
+        qkv = linear(hidden_states, self.qkv_weight)
         q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
@@ -58,7 +61,7 @@ class Qwen3Attention(nn.Module):
             attn = self.paged_attn(q, key_cache, value_cache, attn_metadata.block_tables, attn_metadata.context_lens,
                                    max_context_len=getattr(attn_metadata, "max_context_bound", None),
                                    workspace=getattr(attn_metadata, "decode_workspace", None))
-        return F.linear(attn.reshape(t, self.q_size), self.o_weight)
+        return linear(attn.reshape(t, self.q_size), self.o_weight, skinny=False)
 
 
 class Qwen3MLP(nn.Module):
@@ -69,7 +72,7 @@ class Qwen3MLP(nn.Module):
         self.down_weight = nn.Parameter(torch.empty(config.hidden_size, config.intermediate_size))
 
     def forward(self, x):
-        return F.linear(_C.silu_mul(F.linear(x, self.gate_up_weight)), self.down_weight)
+        return linear(gate_up_silu(x, self.gate_up_weight), self.down_weight, skinny=False)
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -122,7 +125,7 @@ class Qwen3ForCausalLM(nn.Module):
         h = self.model(input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill)
         if logits_indices is not None:
             h = h.index_select(0, logits_indices)
-        return CausalLMOutput(logits=F.linear(h, self.lm_head))
+        return CausalLMOutput(logits=linear(h, self.lm_head, skinny=False))
 
     # ---------------------------------------------------------------- weights
     @torch.no_grad()

@@ -62,3 +62,25 @@ def test_argmax_rows_first_index_on_ties(device):
     torch.cuda.synchronize()
     assert out.tolist() == logits.float().argmax(dim=-1).tolist()
     assert out[3].item() == 100 and out[7].item() == 151935 and out[9].item() == 0
+
+
+@pytest.mark.gpu
+def test_argmax_rows_ragged_vocab_and_ties_within_a_thread(device):
+    """A vocab that is not a multiple of 8 (scalar tail), strided rows, and ties that one thread
+    meets in different load slots of a step or in different steps (the first index wins)."""
+    g = torch.Generator(device=device).manual_seed(2)
+    vocab = 151939
+    buf = _bf((6, 151944), g, device)
+    logits = buf[:, :vocab]
+    logits[0, 8] = 7.0
+    logits[0, 8 + 8192] = 7.0        # same thread, next load slot
+    logits[1, 24] = 7.0
+    logits[1, 24 + 4 * 8192] = 7.0   # same thread, next step
+    logits[2, vocab - 1] = 7.0       # scalar tail
+    logits[3, vocab - 3] = 7.0
+    logits[3, 5] = 7.0               # tie between the vector body and the tail
+    buf[4, vocab:] = 50.0            # padding past vocab is never read as a logit
+    logits[5].fill_(-1.0)
+    out = _C.argmax_rows(logits)
+    torch.cuda.synchronize()
+    assert out.tolist() == [8, 24, vocab - 1, 5, logits[4].float().argmax().item(), 0]
