@@ -201,26 +201,45 @@ int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
                       int vocab, int64_t *out, hipStream_t stream);
 
 /* ------------------------------------------------------------------------- */
-/* Skinny-M projections of the decode step (M <= 32 rows), a weight stream:   */
-/* linear: y[m, n] = bf16(sum_k x[m, k] * w[n, k]), fp32 accumulation.  The   */
-/*   decoder's qkv / o / down projections and the LM head at decode batch     */
-/*   sizes (F.linear at nv/models/qwen3.py:26-35, 48-51, 119 and              */
-/*   nv/layers/embed_head.py:24-39).  n % 32 == 0, k % 256 == 0, x and w      */
-/*   16-byte aligned with row strides (elements) that are multiples of 8.     */
-/* linear_silu_mul: y[m, i] = bf16(bf16(silu(g)) * u), g = bf16(x . w[i]),    */
-/*   u = bf16(x . w[inter + i]) over the fused [2 * inter, k] gate/up weight  */
-/*   (nv/models/qwen3.py:34-35): the gate/up projection and silu_mul in one   */
-/*   launch, with the same rounding points.  inter % 32 == 0.                 */
-/* Both return NVAMD_EUNSUPPORTED for m > 32 (use a library GEMM there).       */
+/* Skinny-M projections of the decode step (m <= 32 rows), a weight stream:   */
+/*   acc[r, c] = sum_k a[r, k] * w[c, k] (fp32), for the decoder's qkv / o /  */
+/*   gate_up / down projections and the LM head at decode batch sizes        */
+/*   (F.linear at nv/models/qwen3.py:26-35, 48-51, 119 and                    */
+/*   nv/layers/embed_head.py:24-39), with the residual add + RMSNorm of the   */
+/*   decoder layer (nv/models/qwen3.py:138-150, nv/layers/layernorm.py:12-17) */
+/*   folded into the GEMMs on either side of it.                              */
+/* Prologue: with x_ssq == NULL, a = x.  Otherwise x is the residual stream,  */
+/*   x_ssq[r * (k/32) + t] holds the sum of squares of x[r, 32t..32t+31], and */
+/*   a = bf16((x * rsqrt(sum_t x_ssq / k + eps)) * norm_weight); k <= 4096.  */
+/* epilogue 0 (store): y[r, c] = bf16(acc).                                   */
+/* epilogue 1 (silu_mul): w is the fused [2n, k] gate/up weight;              */
+/*   y[r, c] = bf16(bf16(silu(bf16(acc_gate))) * bf16(acc_up)).               */
+/* epilogue 2 (residual): y is the residual stream, updated in place:         */
+/*   y[r, c] = bf16(y[r, c] + bf16(acc)); y_ssq[r * (n/32) + t] = sum of      */
+/*   squares of the new y[r, 32t..32t+31] (the next prologue's x_ssq).        */
+/* n % 32 == 0, k % 256 == 0; x, w, x_ssq, norm_weight 16-byte aligned, y     */
+/* 8-byte aligned; row strides in elements (x, w: multiples of 8; y: of 4).   */
+/* Shapes that split K over workgroups need a zero-filled workspace of        */
+/* nvamd_skinny_linear_workspace_size(n, k, epilogue) bytes (0: none); calls  */
+/* leave it zero-filled and must not overlap.  m > 32: NVAMD_EUNSUPPORTED.   */
+/* embed_rows: out[r] = table[ids[r]] (zeros for an id outside [0, vocab)),   */
+/*   the token embedding (torch.embedding at nv/layers/embed_head.py:20-21),  */
+/*   and, if ssq != NULL, ssq[r * (hidden/32) + t] = sum of squares of        */
+/*   out[r, 32t..32t+31].  hidden % 1024 == 0.                                */
 /* ------------------------------------------------------------------------- */
-int nvamd_linear(const void *x, int64_t x_stride, const void *w,
-                 int64_t w_stride, void *y, int64_t y_stride, int m, int n,
-                 int k, hipStream_t stream);
+size_t nvamd_skinny_linear_workspace_size(int n, int k, int epilogue);
 
-int nvamd_linear_silu_mul(const void *x, int64_t x_stride,
-                          const void *w_gate_up, int64_t w_stride, void *y,
-                          int64_t y_stride, int m, int inter, int k,
-                          hipStream_t stream);
+int nvamd_skinny_linear(const void *x, int64_t x_stride, const float *x_ssq,
+                        const void *norm_weight, float eps, const void *w,
+                        int64_t w_stride, void *y, int64_t y_stride,
+                        float *y_ssq, int epilogue, int m, int n, int k,
+                        void *workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+int nvamd_embed_rows(const int64_t *ids, const void *table,
+                     int64_t table_stride, int vocab, void *out,
+                     int64_t out_stride, float *ssq, int rows, int hidden,
+                     hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -56,9 +56,13 @@ _SIGNATURES = {
     "nvamd_add_rms_norm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_float, _c_ptr]),
     "nvamd_silu_mul": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
     "nvamd_argmax_rows": (_c_int, [_c_ptr, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr]),
-    "nvamd_linear": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_int, _c_ptr]),
-    "nvamd_linear_silu_mul": (
-        _c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_int, _c_ptr]),
+    "nvamd_skinny_linear_workspace_size": (_c_size, [_c_int, _c_int, _c_int]),
+    "nvamd_skinny_linear": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_float, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_int, _c_int, _c_int,
+         _c_int, _c_ptr, _c_size, _c_ptr]),
+    "nvamd_embed_rows": (
+        _c_int, [_c_ptr, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_int, _c_int, _c_ptr]),
     "nvamd_qk_norm_rope": (
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr,
@@ -355,37 +359,74 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
 
 
 SKINNY_MAX_ROWS = 32  # rows the skinny projection kernels take (decode batches)
+EPI_STORE, EPI_SILU, EPI_RESID = 0, 1, 2
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """x[M, K] @ w[N, K]^T in bf16 for M <= 32 (HIP skinny GEMM)."""
+def skinny_linear_workspace_size(n: int, k: int, epilogue: int = EPI_STORE) -> int:
+    """Bytes of zero-filled workspace a skinny projection of this shape needs (0: none)."""
+    return int(load().nvamd_skinny_linear_workspace_size(n, k, epilogue))
+
+
+def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, *, epilogue: int = EPI_STORE,
+                  x_ssq: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                  y_ssq: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode-batch projection x[M, K] @ w^T (M <= 32) with an optional RMSNorm prologue and a store,
+    SiLU*mul or residual-add epilogue (one HIP launch).  Returns the output (the residual for EPI_RESID)."""
     lib = load()
     _bf16_cuda("x", x)
     _bf16_cuda("w", w)
     m, k = x.shape
-    n = w.shape[0]
     _require(w.shape[1] == k, "w must be [N, K]")
+    n = w.shape[0] // 2 if epilogue == EPI_SILU else w.shape[0]
+    if epilogue == EPI_RESID:
+        _require(out is not None, "the residual epilogue updates `out` in place")
+        _require(y_ssq is not None and y_ssq.dtype == torch.float32 and y_ssq.is_contiguous()
+                 and y_ssq.numel() >= m * (n // 32), "y_ssq must be fp32 [M, N/32]")
     out = torch.empty((m, n), dtype=x.dtype, device=x.device) if out is None else out
     _require(out.shape == (m, n) and out.dtype == torch.bfloat16 and out.stride(1) == 1, "out must be bf16 [M, N]")
-    status = lib.nvamd_linear(x.data_ptr(), _row_stride(x), w.data_ptr(), _row_stride(w), out.data_ptr(),
-                              out.stride(0), m, n, k, _stream())
-    _check(status, "nvamd_linear")
+    if x_ssq is not None:
+        _require(norm_weight is not None and norm_weight.dtype == torch.bfloat16 and norm_weight.numel() == k,
+                 "norm_weight must be bf16 [K]")
+        _require(x_ssq.dtype == torch.float32 and x_ssq.is_contiguous() and x_ssq.numel() >= m * (k // 32),
+                 "x_ssq must be fp32 [M, K/32]")
+    need = skinny_linear_workspace_size(n, k, epilogue) if n % 32 == 0 and k % 256 == 0 else 0
+    if need and workspace is None:
+        workspace = torch.zeros(need, dtype=torch.uint8, device=x.device)
+    status = lib.nvamd_skinny_linear(
+        x.data_ptr(), _row_stride(x), _ptr(x_ssq), _ptr(norm_weight), float(eps), w.data_ptr(), _row_stride(w),
+        out.data_ptr(), out.stride(0), _ptr(y_ssq), int(epilogue), m, n, k, _ptr(workspace),
+        workspace.numel() if workspace is not None else 0, _stream())
+    _check(status, "nvamd_skinny_linear")
     return out
 
 
-def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
+           workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """x[M, K] @ w[N, K]^T in bf16 for M <= 32 (HIP skinny GEMM)."""
+    return skinny_linear(x, w, out, workspace=workspace)
+
+
+def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor, out: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
     """silu(x @ w_gate_up[:I]^T) * (x @ w_gate_up[I:]^T) in bf16 for M <= 32 (one HIP launch)."""
+    _require(w_gate_up.shape[0] % 2 == 0, "w_gate_up must be [2I, K]")
+    return skinny_linear(x, w_gate_up, out, epilogue=EPI_SILU, workspace=workspace)
+
+
+def embed_rows(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None = None,
+               ssq: torch.Tensor | None = None) -> torch.Tensor:
+    """table[ids] (zero rows for ids outside the vocab) and, if given, per-32-column sums of squares."""
     lib = load()
-    _bf16_cuda("x", x)
-    _bf16_cuda("w_gate_up", w_gate_up)
-    m, k = x.shape
-    two_i = w_gate_up.shape[0]
-    _require(w_gate_up.shape[1] == k and two_i % 2 == 0, "w_gate_up must be [2I, K]")
-    inter = two_i // 2
-    out = torch.empty((m, inter), dtype=x.dtype, device=x.device) if out is None else out
-    _require(out.shape == (m, inter) and out.dtype == torch.bfloat16 and out.stride(1) == 1,
-             "out must be bf16 [M, I]")
-    status = lib.nvamd_linear_silu_mul(x.data_ptr(), _row_stride(x), w_gate_up.data_ptr(), _row_stride(w_gate_up),
-                                       out.data_ptr(), out.stride(0), m, inter, k, _stream())
-    _check(status, "nvamd_linear_silu_mul")
+    _bf16_cuda("table", table)
+    _require(ids.dtype == torch.int64 and ids.is_cuda and ids.is_contiguous(), "ids must be int64 on the GPU")
+    rows = ids.numel()
+    vocab, hidden = table.shape
+    out = torch.empty((rows, hidden), dtype=table.dtype, device=table.device) if out is None else out
+    _require(out.shape == (rows, hidden) and out.dtype == torch.bfloat16, "out must be bf16 [rows, hidden]")
+    if ssq is not None:
+        _require(ssq.dtype == torch.float32 and ssq.is_contiguous() and ssq.numel() >= rows * (hidden // 32),
+                 "ssq must be fp32 [rows, hidden/32]")
+    status = lib.nvamd_embed_rows(ids.data_ptr(), table.data_ptr(), _row_stride(table), vocab, out.data_ptr(),
+                                  _row_stride(out), _ptr(ssq), rows, hidden, _stream())
+    _check(status, "nvamd_embed_rows")
     return out

@@ -7,6 +7,9 @@
 //                 (nv/models/qwen3.py:34-35)
 //   argmax_rows   greedy token of each logits row, first index on ties
 //                 (torch.argmax at nv/layers/sampler.py:13-14)
+//   embed_rows    token embedding gather (torch.embedding at nv/layers/embed_head.py:20-21,
+//                 nv/models/qwen3.py:176) plus the per-32-column sums of squares that the
+//                 first decoder layer's normalising GEMM prologue reads
 // Rounding points match the reference's bf16 model: the residual sum is rounded
 // to bf16, the norm is computed in fp32 with one rounding, silu is rounded to
 // bf16 before the product, which is rounded again.
@@ -152,6 +155,37 @@ argmax_rows_kernel(const u16 *__restrict__ logits, int64_t row_stride, int vocab
   }
 }
 
+// One wave per row: out[r] = table[ids[r]] (a zero row for an id outside [0, vocab)),
+// and ssq[r][t] = sum of squares of columns 32t..32t+31.  Lane l holds columns
+// 16l..16l+15 of each 1024-wide chunk; lanes 2t and 2t+1 make up tile t.
+__global__ void __launch_bounds__(256)
+embed_rows_kernel(const int64_t *__restrict__ ids, const u16 *__restrict__ table, int64_t table_stride, int vocab,
+                  u16 *__restrict__ out, int64_t out_stride, float *__restrict__ ssq, int rows, int hidden) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t id = ids[row];
+  const bool valid = id >= 0 && id < vocab;
+  const u16 *src = table + (valid ? id : 0) * table_stride;
+  u16 *dst = out + (int64_t)row * out_stride;
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  for (int ch = 0; ch < hidden; ch += 1024) {
+    const int off = ch + 16 * lane;
+    const u32x4 a = valid ? ld16(src + off) : z;
+    const u32x4 b = valid ? ld16(src + off + 8) : z;
+    st16(dst + off, a);
+    st16(dst + off + 8, b);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ss += bf16_lo(a[e]) * bf16_lo(a[e]) + bf16_hi(a[e]) * bf16_hi(a[e]);
+      ss += bf16_lo(b[e]) * bf16_lo(b[e]) + bf16_hi(b[e]) * bf16_hi(b[e]);
+    }
+    ss += dpp<kDppQuadXor1>(ss);
+    if (ssq && (lane & 1) == 0) ssq[(int64_t)row * (hidden >> 5) + (off >> 5)] = ss;
+  }
+}
+
 }  // namespace
 }  // namespace nvamd
 
@@ -197,5 +231,19 @@ extern "C" int nvamd_argmax_rows(const void *logits, int64_t row_stride, int row
     return NVAMD_EINVAL;
   hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(kArgmaxThreads), 0, stream, static_cast<const u16 *>(logits),
                      row_stride, vocab, out);
+  return launch_status();
+}
+
+extern "C" int nvamd_embed_rows(const int64_t *ids, const void *table, int64_t table_stride, int vocab, void *out,
+                                int64_t out_stride, float *ssq, int rows, int hidden, hipStream_t stream) {
+  if (rows == 0) return NVAMD_OK;
+  if (!ids || !table || !out || rows < 0 || vocab <= 0) return NVAMD_EINVAL;
+  if (hidden <= 0 || hidden % 1024) return NVAMD_EUNSUPPORTED;
+  if (!aligned16(table) || !aligned16(out) || table_stride < hidden || table_stride % 8 || out_stride < hidden ||
+      out_stride % 8)
+    return NVAMD_EINVAL;
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, ids,
+                     static_cast<const u16 *>(table), table_stride, vocab, static_cast<u16 *>(out), out_stride, ssq,
+                     rows, hidden);
   return launch_status();
 }

@@ -1,167 +1,342 @@
-// Skinny-M projections for decode batches (M <= 32 rows): Y[M, N] = X[M, K] . W[N, K]^T,
-// the per-layer qkv / o / gate_up / down projections and the LM head of the decode step
-// (nv/models/qwen3.py:26-35, 48-51, 119; nv/layers/embed_head.py:24-39).  At M <= 32 the
-// product is a weight stream (2 B of W per 2*M FLOP), so the kernel is built to read W
-// once at HBM rate:
-//   * one workgroup owns 32 output columns (32 rows of W); its NW waves split K, so a
-//     launch keeps N/32 * NW waves and every W byte in flight from the start;
-//   * v_mfma_f32_32x32x16_bf16 with A = the batch rows of X (rows past M repeat row
-//     M-1 and are dropped) and B = 32 rows of W.  Lane (col, kh) feeds A row col and B
-//     column col with the same 8 k's, so it reads 64 contiguous bytes of one W row per
-//     64-wide K block and a row's 128-byte lines come whole;
-//   * the waves' partial 32x32 tiles are added in LDS in a fixed order (deterministic),
-//     then rounded to bf16 once, as a bf16 GEMM with fp32 accumulation does.
-// The SILU variant computes the gate columns n and up columns inter + n of the fused
-// gate/up weight in one workgroup and writes silu(gate) * up (nv/models/qwen3.py:34-35):
-// gate and up are rounded to bf16, silu(gate) is rounded to bf16, the product is rounded
-// again -- the rounding points of the unfused projection + silu_mul.
+// Skinny-M projections of the decode step (M <= 32 rows): Y[M, N] = X[M, K] . W[N, K]^T
+// for the per-layer qkv / o / gate_up / down projections and the LM head
+// (F.linear at nv/models/qwen3.py:26-35, 48-51, 119; nv/layers/embed_head.py:24-39),
+// with the decoder's residual-add + RMSNorm folded into the GEMMs on either side of it
+// (nv/models/qwen3.py:138-150; npu_rms_norm at nv/layers/layernorm.py:12-17).
+//
+// At M <= 32 a projection is a weight stream (2 B of W per 2*M FLOP), so the kernel is
+// shaped to keep every W byte in flight at once, read it once, and keep the per-CU
+// address path at full rate:
+//   * v_mfma_f32_16x16x32_bf16 with A = 16 batch rows of X (one or two M tiles; rows
+//     past M repeat row M-1 and are dropped) and B = 16 rows of W.  Lane (n, g) feeds
+//     column n with k = 8g..8g+7 of each 32-wide step, so one load instruction covers
+//     16 rows x 64 contiguous bytes: 16 whole 64-byte segments per KB of data;
+//   * a workgroup of NW waves owns 16*NT output columns and one of KS slices of K
+//     (split-K across workgroups where the column count alone gives too few
+//     workgroups); its waves split the slice again, and a wave's NT column tiles share
+//     each A fragment;
+//   * the waves' partial tiles meet in LDS; with KS > 1 the workgroups publish fp32
+//     partials with agent-scope write-through stores, count arrivals per column group,
+//     and the last to arrive adds the KS partials in slice order.  Every sum has a
+//     fixed order, so results are deterministic (graph replays equal eager calls).
+//
+// Prologue NORM: X is a residual stream and the A operand is RMSNorm(X) * norm_w, from
+// per-32-column sums of squares of X written by the producer of X (the RESID epilogue or
+// nvamd_embed_rows): rstd = rsqrt(sum / K + eps), a = bf16((x * rstd) * w) -- the rounding
+// of the standalone add_rms_norm kernel.
+// Epilogues: STORE y = bf16(acc); SILU y = bf16(bf16(silu(bf16(gate))) * bf16(up)) from
+// gate rows n and up rows inter + n of the fused gate/up weight (nv/models/qwen3.py:34-35);
+// RESID residual = bf16(residual + bf16(acc)) in place, plus the new per-32-column sums
+// of squares for the next NORM prologue.
 #include "common.h"
 
 namespace nvamd {
 namespace {
 
+enum Epilogue { kEpiStore = 0, kEpiSilu = 1, kEpiResid = 2 };
+
+constexpr int kCounterSlots = 4096;    // arrival counters at the front of the workspace
+constexpr size_t kCounterBytes = kCounterSlots * sizeof(int);
+constexpr int kMaxNormK = 2048;  // NORM prologue: k <= 2048
+constexpr int kSsqVec = kMaxNormK / 128 / 4;  // 16-byte partial-sum loads per lane
+
 struct GemmArgs {
   const u16 *x;
   int64_t x_stride;
+  const float *x_ssq;       // NORM: [m][k / 32]
+  const u16 *norm_w;        // NORM: [k]
+  float eps;
   const u16 *w;
   int64_t w_stride;
-  u16 *y;
+  u16 *y;                   // STORE / SILU output; RESID: the residual, updated in place
   int64_t y_stride;
+  float *y_ssq;             // RESID: [m][n / 32]
   int m;
+  int n;                    // output columns (SILU: inter)
   int k;
-  int up_offset;  // W rows between a gate row and its up row (SILU only)
+  int ks;                   // K slices
+  int k_slice;              // K per slice
+  float *partials;
+  int *counters;
 };
-
-__device__ __forceinline__ f32x16 mfma32(bf16x8v a, bf16x8v b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
-template <int NW, int KB, bool SILU>
+__device__ __forceinline__ void store_agent4(float *p, f32x4 v) {
+  const uint64_t lo = (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32);
+  const uint64_t hi = (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(p) + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 load_agent4(const float *p) {
+  uint64_t *q = reinterpret_cast<uint64_t *>(const_cast<float *>(p));
+  const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return f32x4{__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+               __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32))};
+}
+
+// One 32-wide K step of a wave: W tiles wv[t], X M-tiles xv[mt] (already normalised).
+template <int NACC, int MT>
+__device__ __forceinline__ void mfma_step(f32x4 (&acc)[NACC][MT], const u32x4 (&xa)[MT], const u32x4 *wv) {
+#pragma unroll
+  for (int t = 0; t < NACC; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xa[mt]),
+                                                          __builtin_bit_cast(bf16x8v, wv[t]), acc[t][mt], 0, 0, 0);
+}
+
+template <int NW, int KB, int NT, int MT, int EPI, bool NORM>
 __global__ void __launch_bounds__(NW * 64)
 skinny_gemm_kernel(GemmArgs a) {
-  constexpr int WK = 64 * KB;     // K per wave per round
-  constexpr int RK = NW * WK;     // K per workgroup per round
-  constexpr int NACC = SILU ? 2 : 1;
+  constexpr int kNW = NW;
+  constexpr int NACC = (EPI == kEpiSilu ? 2 : 1) * NT;  // 16-column tiles (SILU: NT gate, then NT up)
+  constexpr int CW = 16 * NT;                           // output columns of the workgroup
+  constexpr int WK = 32 * KB;                           // K per wave per round
+  constexpr int RK = kNW * WK;                          // K per workgroup per round
+  constexpr int TF = 32 * 16;                           // floats of one 32-row x 16-column tile
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31;
-  const int kh = lane >> 5;
-  const int n0 = blockIdx.x * 32;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int group = blockIdx.x / a.ks;
+  const int slice = blockIdx.x - group * a.ks;
+  const int n0 = group * CW;
 
-  const u16 *xp = a.x + (int64_t)min(col, a.m - 1) * a.x_stride + 32 * kh;
+  int xr[MT];
+  const u16 *xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    xr[mt] = min(16 * mt + n, a.m - 1);
+    xp[mt] = a.x + (int64_t)xr[mt] * a.x_stride + 8 * g;
+  }
   const u16 *wp[NACC];
-  wp[0] = a.w + (int64_t)(n0 + col) * a.w_stride + 32 * kh;
-  if (SILU) wp[NACC - 1] = wp[0] + (int64_t)a.up_offset * a.w_stride;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    wp[t] = a.w + (int64_t)(n0 + 16 * t + n) * a.w_stride + 8 * g;
+    if (EPI == kEpiSilu) wp[NT + t] = wp[t] + (int64_t)a.n * a.w_stride;
+  }
+  const u16 *np = NORM ? a.norm_w + 8 * g : nullptr;
 
-  f32x16 acc[NACC];
+  // NORM: the four lanes of a row (g = 0..3) each read a quarter of its k/32 partial sums
+  // of squares (k <= 2048: at most four 16-byte loads).  They are issued before the weight
+  // loads, so rstd is ready while the weights are in flight.
+  float rstd[MT];
+  f32x4 sv[MT][kSsqVec];
+  const int ssq_q = a.k >> 7;  // partials per lane
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    rstd[mt] = 1.f;
+    if (NORM) {
+      const float *sp = a.x_ssq + (int64_t)xr[mt] * (a.k >> 5) + g * ssq_q;
+#pragma unroll
+      for (int i = 0; i < kSsqVec; ++i)
+        sv[mt][i] = 4 * i < ssq_q ? *reinterpret_cast<const f32x4 *>(sp + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  f32x4 acc[NACC][MT];
 #pragma unroll
   for (int t = 0; t < NACC; ++t)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[t][i] = 0.f;
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const int k_begin = slice * a.k_slice;
+  const int k_end = k_begin + a.k_slice;
+  const int k_first = k_begin + w * WK;
 #pragma unroll 1
-  for (int k0 = w * WK; k0 < a.k; k0 += RK) {
-    u32x4 wv[NACC][KB][4], xv[KB][4];
+  for (int k0 = k_first; k0 < k_end; k0 += RK) {
+    u32x4 wv[KB][NACC], xv[KB][MT], nv[NORM ? KB : 1];
 #pragma unroll
-    for (int b = 0; b < KB; ++b)
+    for (int b = 0; b < KB; ++b) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int t = 0; t < NACC; ++t) wv[b][t] = ld16(wp[t] + k0 + 32 * b);
 #pragma unroll
-        for (int t = 0; t < NACC; ++t) wv[t][b][j] = ld16(wp[t] + k0 + 64 * b + 8 * j);
-        xv[b][j] = ld16(xp + k0 + 64 * b + 8 * j);
-      }
+      for (int mt = 0; mt < MT; ++mt) xv[b][mt] = ld16(xp[mt] + k0 + 32 * b);
+      if (NORM) nv[b] = ld16(np + k0 + 32 * b);
+    }
     // every load of the round is issued before the first MFMA waits on one
     __builtin_amdgcn_sched_barrier(0);
+    if (NORM && k0 == k_first) {
 #pragma unroll
-    for (int b = 0; b < KB; ++b)
+      for (int mt = 0; mt < MT; ++mt) {
+        float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int i = 0; i < kSsqVec; ++i) ss += (sv[mt][i][0] + sv[mt][i][1]) + (sv[mt][i][2] + sv[mt][i][3]);
+        ss += swizzle_xor16(ss);
+        ss += __shfl_xor(ss, 32);
+        rstd[mt] = rsqrtf(ss / (float)a.k + a.eps);
+      }
+    }
 #pragma unroll
-        for (int t = 0; t < NACC; ++t)
-          acc[t] = mfma32(__builtin_bit_cast(bf16x8v, xv[b][j]), __builtin_bit_cast(bf16x8v, wv[t][b][j]), acc[t]);
+    for (int b = 0; b < KB; ++b) {
+      u32x4 xa[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        xa[mt] = xv[b][mt];
+        if (NORM) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            xa[mt][e] = pack_bf16x2(bf16_lo(xa[mt][e]) * rstd[mt] * bf16_lo(nv[b][e]),
+                                    bf16_hi(xa[mt][e]) * rstd[mt] * bf16_hi(nv[b][e]));
+        }
+      }
+      mfma_step<NACC, MT>(acc, xa, wv[b]);
+    }
   }
 
-  // C register i of lane l is row 8*(i/4) + 4*(l/32) + i%4, column l%32 of the tile.
-  __shared__ float s_c[NW][NACC][32 * 32];
+  // C register i of lane (n, g) in M tile mt is row 16*mt + 4*g + i, column n of the tile.
+  __shared__ float s_c[kNW][NACC][TF];
+  __shared__ int s_last;
 #pragma unroll
   for (int t = 0; t < NACC; ++t)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s_c[w][t][(8 * (i >> 2) + 4 * kh + (i & 3)) * 32 + col] = acc[t][i];
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_c[w][t][(16 * mt + 4 * g + i) * 16 + n] = acc[t][mt][i];
   __syncthreads();
 
-  for (int e = tid; e < 32 * 32; e += NW * 64) {
-    const int row = e >> 5;
-    if (row >= a.m) break;  // e grows with row: nothing further to store
-    float s[NACC];
+  float *part = a.partials + ((int64_t)group * a.ks) * NACC * TF;
+  if (a.ks > 1) {
+    for (int u = tid; u < NACC * TF / 4; u += kNW * 64) {
+      const int t = u / (TF / 4);
+      const int e = 4 * (u % (TF / 4));
+      f32x4 s = *reinterpret_cast<const f32x4 *>(&s_c[0][t][e]);
 #pragma unroll
-    for (int t = 0; t < NACC; ++t) {
-      s[t] = 0.f;
-#pragma unroll
-      for (int x = 0; x < NW; ++x) s[t] += s_c[x][t][e];
+      for (int x = 1; x < kNW; ++x) s += *reinterpret_cast<const f32x4 *>(&s_c[x][t][e]);
+      store_agent4(part + ((int64_t)slice * NACC + t) * TF + e, s);
     }
-    float v;
-    if (SILU) {
-      const float gate = round_bf16(s[0]);
-      const float up = round_bf16(s[NACC - 1]);
-      v = round_bf16(silu_f32(gate)) * up;
-    } else {
-      v = s[0];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keep the stores above the wait
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const int prev = __hip_atomic_fetch_add(a.counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == a.ks - 1;
     }
-    a.y[(int64_t)row * a.y_stride + n0 + (e & 31)] = f32_to_bf16(v);
+    __syncthreads();
+    if (!s_last) return;
   }
+
+  // Work unit u: 4 consecutive columns of one output row; the 8 units of 32 columns of a
+  // row sit in 8 consecutive lanes.
+  constexpr int kRowUnits = CW / 4;
+  for (int u = tid; u < 32 * kRowUnits; u += kNW * 64) {
+    const int row = u / kRowUnits;
+    const int cl = 4 * (u % kRowUnits);  // column inside the workgroup's CW
+    const int t = cl >> 4;
+    const int e = row * 16 + (cl & 15);
+    constexpr int NV = EPI == kEpiSilu ? 2 : 1;
+    f32x4 v[NV];
+#pragma unroll
+    for (int h = 0; h < NV; ++h) {
+      const int tt = t + h * NT;
+      if (a.ks > 1) {
+        v[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < a.ks; s0 += 8) {  // eight slices' loads in flight per step
+          f32x4 ld[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            ld[q] = load_agent4(part + ((int64_t)min(s0 + q, a.ks - 1) * NACC + tt) * TF + e);
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (s0 + q < a.ks) v[h] += ld[q];
+        }
+      } else {
+        v[h] = *reinterpret_cast<const f32x4 *>(&s_c[0][tt][e]);
+#pragma unroll
+        for (int x = 1; x < kNW; ++x) v[h] += *reinterpret_cast<const f32x4 *>(&s_c[x][tt][e]);
+      }
+    }
+    const int c = n0 + cl;
+    u16 *yp = a.y + (int64_t)row * a.y_stride + c;
+    if (EPI == kEpiStore) {
+      if (row < a.m)
+        *reinterpret_cast<u32x2 *>(yp) = u32x2{pack_bf16x2(v[0][0], v[0][1]), pack_bf16x2(v[0][2], v[0][3])};
+    } else if (EPI == kEpiSilu) {
+      float o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = round_bf16(silu_f32(round_bf16(v[0][q]))) * round_bf16(v[NV - 1][q]);
+      if (row < a.m) *reinterpret_cast<u32x2 *>(yp) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    } else {  // RESID
+      const int rr = min(row, a.m - 1);
+      const u32x2 r = *reinterpret_cast<const u32x2 *>(a.y + (int64_t)rr * a.y_stride + c);
+      const u32 h0 = pack_bf16x2(bf16_lo(r[0]) + round_bf16(v[0][0]), bf16_hi(r[0]) + round_bf16(v[0][1]));
+      const u32 h1 = pack_bf16x2(bf16_lo(r[1]) + round_bf16(v[0][2]), bf16_hi(r[1]) + round_bf16(v[0][3]));
+      float ss = bf16_lo(h0) * bf16_lo(h0) + bf16_hi(h0) * bf16_hi(h0) + bf16_lo(h1) * bf16_lo(h1) +
+                 bf16_hi(h1) * bf16_hi(h1);
+      ss = sum8(ss);  // the 8 units of these 32 columns
+      if (row < a.m) {
+        *reinterpret_cast<u32x2 *>(yp) = u32x2{h0, h1};
+        if ((c & 31) == 0) a.y_ssq[(int64_t)row * (a.n >> 5) + (c >> 5)] = ss;
+      }
+    }
+  }
+  if (a.ks > 1 && tid == 0)  // leave the workspace ready for the next call
+    __hip_atomic_store(a.counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waves per workgroup: enough that the launch holds >= 1024 waves, 4..16 (8 for SILU,
-// whose two tiles double the LDS), and dividing K into 64-wide blocks.
-int pick_waves(int tiles, int k, bool silu) {
-  int nw = 4;
-  while (nw < 16 && (int64_t)tiles * nw < 1024) nw *= 2;
-  if (silu && nw > 8) nw = 8;
-  while (nw > 4 && k % (nw * 64) != 0) nw /= 2;
-  return k % (nw * 64) == 0 ? nw : 0;
+struct Plan {
+  int nw, nt, ks, kb;
+};
+
+// Measured on MI355X at M = 32 (graph replay):
+//   * vocabulary-sized N (LM head): 128 columns per 4-wave workgroup, no split;
+//   * residual epilogue (N = hidden: o_proj, down_proj): 32 columns, K split over >= 256
+//     workgroups -- the deterministic cross-workgroup merge costs less than the X
+//     re-reads an unsplit K would need;
+//   * otherwise (qkv, gate_up): 16 columns per 8-wave workgroup, no split.
+Plan make_plan(int n, int k, int epi) {
+  Plan p{8, 1, 1, k % 512 == 0 ? 2 : 1};
+  if (epi == kEpiStore && n % 128 == 0 && n / 128 >= 512) {
+    p = Plan{4, 8, 1, 2};
+  } else if (epi == kEpiResid) {
+    p = Plan{4, 2, 1, 1};
+    const int groups = n / 32;
+    static const int kSlices[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    for (int ks : kSlices) {
+      if (k % ks != 0 || (k / ks) % 128 != 0) continue;
+      p.ks = ks;
+      if (groups * ks >= 256) break;
+    }
+    p.kb = (k / p.ks) % 256 == 0 ? 2 : 1;
+  }
+  return p;
 }
 
-template <int NW, bool SILU>
-int launch_kb(const GemmArgs &a, int tiles, hipStream_t stream) {
-  const int per = a.k / (NW * 64);
-  const dim3 grid(tiles), block(NW * 64);
-  if (per % 2 == 0)
-    hipLaunchKernelGGL((skinny_gemm_kernel<NW, 2, SILU>), grid, block, 0, stream, a);
-  else if (per % 3 == 0)
-    hipLaunchKernelGGL((skinny_gemm_kernel<NW, 3, SILU>), grid, block, 0, stream, a);
+size_t workspace_bytes_for(const Plan &p, int n, int epi) {
+  if (p.ks <= 1) return 0;
+  const int nacc = (epi == kEpiSilu ? 2 : 1) * p.nt;
+  const size_t groups = (size_t)n / (16 * p.nt);
+  return kCounterBytes + groups * p.ks * nacc * 32 * 16 * sizeof(float);
+}
+
+template <int NW, int KB, int NT, int EPI, bool NORM>
+int launch(const GemmArgs &a, int grid, hipStream_t stream) {
+  if (a.m > 16)
+    hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 2, EPI, NORM>), dim3(grid), dim3(NW * 64), 0, stream, a);
   else
-    hipLaunchKernelGGL((skinny_gemm_kernel<NW, 1, SILU>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 1, EPI, NORM>), dim3(grid), dim3(NW * 64), 0, stream, a);
   return launch_status();
 }
 
-int run(const GemmArgs &a, int tiles, bool silu, hipStream_t stream) {
-  const int nw = pick_waves(tiles, a.k, silu);
-  if (silu) {
-    switch (nw) {
-      case 4: return launch_kb<4, true>(a, tiles, stream);
-      case 8: return launch_kb<8, true>(a, tiles, stream);
-      default: return NVAMD_EUNSUPPORTED;
-    }
-  }
-  switch (nw) {
-    case 4: return launch_kb<4, false>(a, tiles, stream);
-    case 8: return launch_kb<8, false>(a, tiles, stream);
-    case 16: return launch_kb<16, false>(a, tiles, stream);
-    default: return NVAMD_EUNSUPPORTED;
-  }
+template <int NW, int NT, int EPI, bool NORM>
+int launch_kb(const GemmArgs &a, const Plan &p, int grid, hipStream_t stream) {
+  return p.kb == 2 ? launch<NW, 2, NT, EPI, NORM>(a, grid, stream) : launch<NW, 1, NT, EPI, NORM>(a, grid, stream);
 }
 
-int check_common(const void *x, int64_t x_stride, const void *w, int64_t w_stride, const void *y, int64_t y_stride,
-                 int m, int n, int k) {
-  if (!x || !w || !y || m < 0 || n <= 0 || k <= 0) return NVAMD_EINVAL;
-  if (m > 32 || n % 32 != 0 || k % 256 != 0) return NVAMD_EUNSUPPORTED;
-  if (!aligned16(x) || !aligned16(w) || x_stride % 8 || w_stride % 8 || x_stride < k || w_stride < k ||
-      y_stride < n || (reinterpret_cast<uintptr_t>(y) & 1u))
-    return NVAMD_EINVAL;
-  return NVAMD_OK;
+template <int EPI, bool NORM>
+int dispatch(const GemmArgs &a, const Plan &p, int grid, hipStream_t stream) {
+  if constexpr (EPI == kEpiStore) {
+    if (p.nw == 4 && p.nt == 8) return launch_kb<4, 8, EPI, NORM>(a, p, grid, stream);
+  }
+  if constexpr (EPI == kEpiResid) {
+    if (p.nw == 4 && p.nt == 2) return launch_kb<4, 2, EPI, NORM>(a, p, grid, stream);
+  } else {
+    if (p.nw == 8 && p.nt == 1) return launch_kb<8, 1, EPI, NORM>(a, p, grid, stream);
+  }
+  return NVAMD_EUNSUPPORTED;
 }
 
 }  // namespace
@@ -169,22 +344,57 @@ int check_common(const void *x, int64_t x_stride, const void *w, int64_t w_strid
 
 using namespace nvamd;
 
-extern "C" int nvamd_linear(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
-                            int64_t y_stride, int m, int n, int k, hipStream_t stream) {
-  if (m == 0) return NVAMD_OK;
-  const int st = check_common(x, x_stride, w, w_stride, y, y_stride, m, n, k);
-  if (st != NVAMD_OK) return st;
-  GemmArgs a{static_cast<const u16 *>(x), x_stride, static_cast<const u16 *>(w), w_stride, static_cast<u16 *>(y),
-             y_stride, m, k, 0};
-  return run(a, n / 32, false, stream);
+extern "C" size_t nvamd_skinny_linear_workspace_size(int n, int k, int epilogue) {
+  if (n <= 0 || k <= 0 || n % 32 || k % 256 || epilogue < 0 || epilogue > 2) return 0;
+  const Plan p = make_plan(n, k, epilogue);
+  return workspace_bytes_for(p, n, epilogue);
 }
 
-extern "C" int nvamd_linear_silu_mul(const void *x, int64_t x_stride, const void *w_gate_up, int64_t w_stride,
-                                     void *y, int64_t y_stride, int m, int inter, int k, hipStream_t stream) {
+extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float *x_ssq, const void *norm_weight,
+                                   float eps, const void *w, int64_t w_stride, void *y, int64_t y_stride,
+                                   float *y_ssq, int epilogue, int m, int n, int k, void *workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
   if (m == 0) return NVAMD_OK;
-  const int st = check_common(x, x_stride, w_gate_up, w_stride, y, y_stride, m, inter, k);
-  if (st != NVAMD_OK) return st;
-  GemmArgs a{static_cast<const u16 *>(x), x_stride, static_cast<const u16 *>(w_gate_up), w_stride,
-             static_cast<u16 *>(y), y_stride, m, k, inter};
-  return run(a, inter / 32, true, stream);
+  if (!x || !w || !y || m < 0 || n <= 0 || k <= 0 || epilogue < 0 || epilogue > 2) return NVAMD_EINVAL;
+  if (m > 32 || n % 32 != 0 || k % 256 != 0) return NVAMD_EUNSUPPORTED;
+  const bool norm = x_ssq != nullptr;
+  if (norm && !norm_weight) return NVAMD_EINVAL;
+  if (norm && k > kMaxNormK) return NVAMD_EUNSUPPORTED;
+  if (epilogue == kEpiResid && !y_ssq) return NVAMD_EINVAL;
+  if (!aligned16(x) || !aligned16(w) || x_stride % 8 || w_stride % 8 || x_stride < k || w_stride < k ||
+      y_stride < n || (reinterpret_cast<uintptr_t>(y) & 7u) || y_stride % 4 ||
+      (norm && (!aligned16(x_ssq) || !aligned16(norm_weight))))
+    return NVAMD_EINVAL;
+  const Plan p = make_plan(n, k, epilogue);
+  const int groups = n / (16 * p.nt);
+  if ((k / p.ks) % (32 * p.kb) != 0) return NVAMD_EUNSUPPORTED;  // whole wave blocks per slice
+  if (p.ks > 1) {
+    if (groups > kCounterSlots) return NVAMD_EUNSUPPORTED;
+    if (!workspace || !aligned16(workspace) || workspace_bytes < workspace_bytes_for(p, n, epilogue))
+      return NVAMD_EWORKSPACE;
+  }
+  GemmArgs a;
+  a.x = static_cast<const u16 *>(x);
+  a.x_stride = x_stride;
+  a.x_ssq = x_ssq;
+  a.norm_w = static_cast<const u16 *>(norm_weight);
+  a.eps = eps;
+  a.w = static_cast<const u16 *>(w);
+  a.w_stride = w_stride;
+  a.y = static_cast<u16 *>(y);
+  a.y_stride = y_stride;
+  a.y_ssq = y_ssq;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.ks = p.ks;
+  a.k_slice = k / p.ks;
+  a.counters = static_cast<int *>(workspace);
+  a.partials = workspace ? reinterpret_cast<float *>(static_cast<char *>(workspace) + kCounterBytes) : nullptr;
+  const int grid = groups * p.ks;
+  switch (epilogue) {
+    case kEpiSilu: return norm ? dispatch<kEpiSilu, true>(a, p, grid, stream) : dispatch<kEpiSilu, false>(a, p, grid, stream);
+    case kEpiResid: return norm ? dispatch<kEpiResid, true>(a, p, grid, stream) : dispatch<kEpiResid, false>(a, p, grid, stream);
+    default: return norm ? dispatch<kEpiStore, true>(a, p, grid, stream) : dispatch<kEpiStore, false>(a, p, grid, stream);
+  }
 }

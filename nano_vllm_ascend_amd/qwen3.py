@@ -4,10 +4,14 @@ Per layer: RMSNorm -> fused qkv projection -> qk_norm_rope (per-head RMSNorm,
 rotate-half RoPE and the KV store of post-RoPE k and raw v, one kernel) ->
 prefill or paged-decode attention -> o_proj -> residual -> RMSNorm -> SwiGLU
 MLP (fused gate/up projection) -> residual.  q/k/v are views into the fused projection
-output, which the kernels accept through their row strides.  At decode batch sizes
-(<= 32 rows) the qkv projection and the gate/up projection + SiLU*mul run on the
-skinny-M HIP GEMM (the latter as one launch); the o/down projections and the LM head
-stay on hipBLASLt, which is faster for their shapes.
+output, which the kernels accept through their row strides.
+
+Decode batches of <= 32 rows take a fused path (``forward_decode_fused``): the
+skinny-M HIP GEMM runs every projection, each RMSNorm in the prologue of the GEMM
+that consumes it, and each residual add in the epilogue of the GEMM that produces
+it (with the per-32-column sums of squares the next norm needs), and SiLU*mul in
+the gate/up epilogue -- 6 launches per layer instead of 9, same rounding points.
+Prefill and larger batches run the unfused chain on hipBLASLt + add_rms_norm.
 """
 from __future__ import annotations
 
@@ -63,6 +67,25 @@ class Qwen3Attention(nn.Module):
                                    workspace=getattr(attn_metadata, "decode_workspace", None))
         return linear(attn.reshape(t, self.q_size), self.o_weight, skinny=False)
 
+    def decode_fused(self, residual, ssq, norm: RMSNorm, rotary, positions, kv_cache, attn_metadata, workspace):
+        """residual += o_proj(attention(qkv_proj(norm(residual)))) in place, for a decode batch of
+        <= 32 rows: the input RMSNorm runs in the qkv GEMM's prologue and the residual add (with
+        the sums of squares the next norm needs) in the o_proj GEMM's epilogue."""
+        t = residual.shape[0]
+        qkv = _C.skinny_linear(residual, self.qkv_weight, x_ssq=ssq, norm_weight=norm.weight,
+                               eps=norm.variance_epsilon, workspace=workspace)
+        q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
+        k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
+        v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
+        qk_norm_rope(q, k, v, self.q_norm, self.k_norm, rotary, positions, kv_cache, self.layer_idx,
+                     attn_metadata.slot_mapping)
+        key_cache, value_cache = kv_cache.get_physical_cache(self.layer_idx)
+        attn = self.paged_attn(q, key_cache, value_cache, attn_metadata.block_tables, attn_metadata.context_lens,
+                               max_context_len=getattr(attn_metadata, "max_context_bound", None),
+                               workspace=getattr(attn_metadata, "decode_workspace", None))
+        _C.skinny_linear(attn.reshape(t, self.q_size), self.o_weight, residual, epilogue=_C.EPI_RESID, y_ssq=ssq,
+                         workspace=workspace)
+
 
 class Qwen3MLP(nn.Module):
     def __init__(self, config: Qwen3Config):
@@ -73,6 +96,14 @@ class Qwen3MLP(nn.Module):
 
     def forward(self, x):
         return linear(gate_up_silu(x, self.gate_up_weight), self.down_weight, skinny=False)
+
+    def decode_fused(self, residual, ssq, norm: RMSNorm, workspace):
+        """residual += down(silu(gate(norm(residual))) * up(norm(residual))) in place (<= 32 rows):
+        norm in the gate/up GEMM's prologue, SiLU*mul in its epilogue, the residual add in the
+        down GEMM's epilogue."""
+        act = _C.skinny_linear(residual, self.gate_up_weight, epilogue=_C.EPI_SILU, x_ssq=ssq,
+                               norm_weight=norm.weight, eps=norm.variance_epsilon, workspace=workspace)
+        _C.skinny_linear(act, self.down_weight, residual, epilogue=_C.EPI_RESID, y_ssq=ssq, workspace=workspace)
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -111,6 +142,21 @@ class Qwen3Model(nn.Module):
             nxt.add_forward(m, residual, x)
         return x
 
+    def forward_decode_fused(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, workspace):
+        """Decode forward for <= 32 rows with every RMSNorm and residual add folded into the
+        projections: 6 launches per layer (qkv, qk_norm_rope, attention, o, gate_up, down).
+        Returns the final residual stream and its per-32-column sums of squares; the final
+        norm runs in the LM head's prologue."""
+        t = input_ids_flat.shape[0]
+        hidden = self.embed_tokens.shape[1]
+        ssq = torch.empty((t, hidden // 32), dtype=torch.float32, device=self.embed_tokens.device)
+        residual = _C.embed_rows(input_ids_flat, self.embed_tokens, ssq=ssq)
+        for layer in self.layers:
+            layer.self_attn.decode_fused(residual, ssq, layer.input_layernorm, self.rotary_emb, position_ids_flat,
+                                         kv_cache, attn_metadata, workspace)
+            layer.mlp.decode_fused(residual, ssq, layer.post_attention_layernorm, workspace)
+        return residual, ssq
+
 
 class Qwen3ForCausalLM(nn.Module):
     def __init__(self, config: Qwen3Config, block_size: int = 128, max_model_len: int = 2048):
@@ -120,12 +166,40 @@ class Qwen3ForCausalLM(nn.Module):
         self.lm_head = self.model.embed_tokens if config.tie_word_embeddings else nn.Parameter(
             torch.empty(config.vocab_size, config.hidden_size))
 
+        self._gemm_workspace = None
+
+    def decode_fusable(self, rows: int) -> bool:
+        """Whether a decode batch of `rows` runs on the fused skinny-GEMM path."""
+        c = self.config
+        dev = self.model.embed_tokens.device
+        return (dev.type == "cuda" and 0 < rows <= _C.SKINNY_MAX_ROWS and c.hidden_size % 1024 == 0
+                and c.hidden_size <= 2048 and c.intermediate_size % 256 == 0
+                and (c.num_attention_heads * c.head_dim) % 256 == 0 and c.vocab_size % 32 == 0)
+
+    def gemm_workspace(self) -> torch.Tensor:
+        """Zero-filled workspace shared by the decode projections (calls run in stream order)."""
+        if self._gemm_workspace is None:
+            c = self.config
+            h, i, q = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim
+            shapes = [(h, q, _C.EPI_RESID), (h, i, _C.EPI_RESID), (i, h, _C.EPI_SILU),
+                      (q + 2 * c.num_key_value_heads * c.head_dim, h, _C.EPI_STORE), (c.vocab_size, h, _C.EPI_STORE)]
+            need = max([_C.skinny_linear_workspace_size(n, k, e) for n, k, e in shapes] + [16])
+            self._gemm_workspace = torch.zeros(need, dtype=torch.uint8, device=self.model.embed_tokens.device)
+        return self._gemm_workspace
+
     def forward(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill: bool,
                 logits_indices=None) -> CausalLMOutput:
+        if not is_prefill and logits_indices is None and self.decode_fusable(input_ids_flat.shape[0]):
+            ws = self.gemm_workspace()
+            residual, ssq = self.model.forward_decode_fused(input_ids_flat, position_ids_flat, kv_cache,
+                                                            attn_metadata, ws)
+            norm = self.model.norm
+            return CausalLMOutput(logits=_C.skinny_linear(residual, self.lm_head, x_ssq=ssq, norm_weight=norm.weight,
+                                                          eps=norm.variance_epsilon, workspace=ws))
         h = self.model(input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill)
         if logits_indices is not None:
             h = h.index_select(0, logits_indices)
-        return CausalLMOutput(logits=linear(h, self.lm_head, skinny=False))
+        return CausalLMOutput(logits=linear(h, self.lm_head))
 
     # ---------------------------------------------------------------- weights
     @torch.no_grad()

@@ -129,3 +129,37 @@ def test_full_depth_model_generates(device):
     assert llm.runner.decode_graph_stats()["captures"] == 1
     del llm
     torch.cuda.empty_cache()
+
+
+@pytest.mark.gpu
+def test_fused_decode_path_matches_unfused_chain(device):
+    """Decode batches <= 32 rows fold every RMSNorm and residual add into the projections; the
+    logits must match the unfused chain (library GEMMs + add_rms_norm) of the same model to
+    rounding, and tokens may differ only at near-ties."""
+    fused, plain = make_llm(graph=False), make_llm(graph=False)
+    plain.runner.model.decode_fusable = lambda rows: False
+    prompts = prompts_for([37, 128, 200, 5], seed=3)
+    for llm in (fused, plain):
+        llm.runner.tokenizer.eos_token_id = -1
+        for p in prompts:
+            llm.submit(p, max_new_tokens=17)
+    worst, steps = 0.0, 0
+    while fused.has_unfinished():
+        fused.step()
+        plain.step()
+        if steps > 0:  # the first step is the (shared, unfused) prefill
+            la, lb = fused.runner.last_logits.float(), plain.runner.last_logits.float()
+            assert la.shape == lb.shape
+            worst = max(worst, (la - lb).abs().max().item())
+        steps += 1
+        ta = [s.next_token_id for s in fused.scheduler.seqs.values()]
+        tb = [s.next_token_id for s in plain.scheduler.seqs.values()]
+        if ta != tb:  # inputs diverge from here on: the differing token must be a near-tie
+            lb = plain.runner.last_logits.float()
+            for row, (x, y) in enumerate(zip(ta, tb)):
+                if x != y:
+                    assert (lb[row, y] - lb[row, x]).item() < TIE_TOL
+            break
+    print(f"fused vs unfused decode: {steps} steps compared, worst logit diff {worst:.4f}")
+    assert fused.runner.model._gemm_workspace is not None and plain.runner.model._gemm_workspace is None
+    assert steps >= 4 and worst <= 0.05
