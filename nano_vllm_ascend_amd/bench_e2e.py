@@ -8,6 +8,16 @@ timed run (prefill included).  The model is the Qwen3-0.6B shape with seeded
 random weights.
 
     python -m nano_vllm_ascend_amd.bench_e2e --prompts 32 --input 256 --output 2048
+
+The load workload -- 100 requests x 2048 / 2048 tokens, half of them sharing one
+seeded 1024-token prefix, prefix cache on (the reference's own run of 100 x
+2048 / 2048 is bench_outputs/nano_100_2048_2048.json) -- is
+
+    python -m nano_vllm_ascend_amd.bench_e2e --prompts 100 --input 2048 --output 2048 \
+        --shared-prefix 1024 --shared-fraction 0.5 --prefix-cache
+
+With the prefix cache on, the warm-up uses a different seed and the cache is
+cleared before the timed run, so only the intended sharing can hit.
 """
 from __future__ import annotations
 
@@ -23,10 +33,18 @@ from .engine import LLM
 from .sequence import Sequence
 
 
-def make_dataset(num_prompts: int, input_len: int, vocab_size: int, seed: int, token_id_high: int = 10000):
+def make_dataset(num_prompts: int, input_len: int, vocab_size: int, seed: int, token_id_high: int = 10000,
+                 shared_prefix: int = 0, shared_fraction: float = 0.0):
+    """Random prompts; the first round(shared_fraction * N) of them start with one common
+    `shared_prefix`-token prefix (seeded too)."""
     rng = random.Random(seed)
     high = min(token_id_high, vocab_size - 1)
-    return [[rng.randint(0, high) for _ in range(input_len)] for _ in range(num_prompts)]
+    prompts = [[rng.randint(0, high) for _ in range(input_len)] for _ in range(num_prompts)]
+    if shared_prefix > 0 and shared_fraction > 0:
+        prefix = [rng.randint(0, high) for _ in range(min(shared_prefix, input_len))]
+        for p in prompts[: round(shared_fraction * num_prompts)]:
+            p[: len(prefix)] = prefix
+    return prompts
 
 
 def generate_from_token_ids(llm: LLM, prompts: list[list[int]], output_len: int, sampling_params=None):
@@ -53,29 +71,43 @@ def generate_from_token_ids(llm: LLM, prompts: list[list[int]], output_len: int,
 
 def run_e2e(num_prompts: int = 32, input_len: int = 256, output_len: int = 2048, seed: int = 0, device=None,
             max_model_len: int = 4096, block_size: int = 128, warmup: int = 1, num_blocks: int | None = None,
-            enable_decode_graph: bool = True, llm: LLM | None = None) -> dict:
+            enable_decode_graph: bool = True, llm: LLM | None = None, shared_prefix: int = 0,
+            shared_fraction: float = 0.0, enable_prefix_cache: bool = False) -> dict:
     cfg = QWEN3_0_6B
     need = num_prompts * -(-(input_len + output_len) // block_size)
     if llm is None:
         llm = LLM(cfg, max_model_len=max_model_len, block_size=block_size, num_blocks=num_blocks or need + 64,
-                  max_num_seqs=num_prompts, enable_decode_graph=enable_decode_graph, seed=seed)
+                  max_num_seqs=num_prompts, enable_decode_graph=enable_decode_graph, seed=seed,
+                  enable_prefix_cache=enable_prefix_cache)
     llm.runner.tokenizer.eos_token_id = -1  # ignore EOS, as the reference benchmark does
-    prompts = make_dataset(num_prompts, input_len, cfg.vocab_size, seed)
-    for _ in range(warmup):
-        generate_from_token_ids(llm, prompts, output_len)
+    prompts = make_dataset(num_prompts, input_len, cfg.vocab_size, seed, shared_prefix=shared_prefix,
+                           shared_fraction=shared_fraction)
+    for w in range(warmup):
+        warm = prompts if not enable_prefix_cache else make_dataset(
+            num_prompts, input_len, cfg.vocab_size, seed + 1 + w, shared_prefix=shared_prefix,
+            shared_fraction=shared_fraction)
+        generate_from_token_ids(llm, warm, output_len)
         torch.cuda.synchronize()
+    if enable_prefix_cache:
+        llm.clear_prefix_cache()
     t0 = time.perf_counter()
     outs = generate_from_token_ids(llm, prompts, output_len)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     generated = sum(len(o) for o in outs)
+    workload = f"{num_prompts}x{input_len}/{output_len} greedy ignore_eos"
+    if shared_prefix and shared_fraction:
+        workload += f", {shared_fraction:g} of requests share a {shared_prefix}-token prefix"
+    if enable_prefix_cache:
+        workload += ", prefix cache on"
     return {
-        "workload": f"{num_prompts}x{input_len}/{output_len} greedy ignore_eos",
+        "workload": workload,
         "output_tok_s": round(generated / elapsed, 2),
         "total_tok_s": round((generated + num_prompts * input_len) / elapsed, 2),
         "elapsed_s": round(elapsed, 3),
         "generated_tokens": generated,
         "decode_graph": llm.runner.decode_graph_stats(),
+        "overlapped_steps": dict(llm.runner.overlap_stats),
         "model": "Qwen3-0.6B shape, seeded N(0, 0.02) weights, bf16",
     }
 
@@ -88,9 +120,15 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--shared-prefix", type=int, default=0, help="tokens of the common prefix")
+    ap.add_argument("--shared-fraction", type=float, default=0.0, help="fraction of requests that share it")
+    ap.add_argument("--prefix-cache", action="store_true")
+    ap.add_argument("--max-model-len", type=int, default=4096)
     args = ap.parse_args()
     print(json.dumps(run_e2e(args.prompts, args.input, args.output, args.seed, warmup=args.warmup,
-                             enable_decode_graph=not args.no_graph)))
+                             enable_decode_graph=not args.no_graph, shared_prefix=args.shared_prefix,
+                             shared_fraction=args.shared_fraction, enable_prefix_cache=args.prefix_cache,
+                             max_model_len=args.max_model_len)))
 
 
 if __name__ == "__main__":

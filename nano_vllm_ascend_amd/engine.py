@@ -59,7 +59,9 @@ class LLM:
     found are initialised from N(0, 0.02) with a fixed seed.  The remaining
     arguments keep the reference's names and defaults (nv/engine.py:59-71);
     ``npu_memory_utilization`` is the fraction of device memory the KV pool
-    may grow to when ``num_blocks`` is not given.
+    may grow to when ``num_blocks`` is not given.  ``enable_overlap`` (not in
+    the reference) lets the runner launch a decode step while the host still
+    processes the previous one's tokens; outputs are unchanged.
     """
 
     def __init__(
@@ -75,6 +77,7 @@ class LLM:
         enable_decode_graph: bool = True,
         decode_graph_batch_sizes: list[int] | None = None,
         seed: int = 0,
+        enable_overlap: bool = True,
     ):
         from .model_runner import ModelRunner
 
@@ -90,6 +93,7 @@ class LLM:
             decode_graph_batch_sizes=decode_graph_batch_sizes,
             seed=seed,
             max_num_seqs=max_num_seqs,
+            enable_overlap=enable_overlap,
         )
         self.scheduler = MiniScheduler(
             max_num_seqs=max_num_seqs,

@@ -7,7 +7,17 @@ Differences from the reference, all on the hot path:
   - decode at a captured batch size packs straight into the graph's static
     buffers, so a replay needs no device-to-device input copies;
   - greedy sampling of a batch is one argmax and ONE device-to-host read per
-    step (the reference synchronised once per sequence).
+    step (the reference synchronised once per sequence);
+  - overlapped decode: when step N+1's inputs are fully determined before
+    step N's tokens reach the host (every sequence continues, nothing was
+    prefilled in between, greedy sampling, a captured batch size), step N+1
+    is launched right behind step N with its input ids copied on the device
+    from step N's argmax.  The host then reads step N's tokens and runs the
+    scheduler while the GPU computes step N+1.  The next call checks that the
+    batch it was asked for is the one launched (same sequences, same
+    positions) and otherwise launches normally; a discarded step only
+    rewrote identical K/V values or slots of finished sequences.  Outputs are
+    those of the synchronous loop.
 """
 from __future__ import annotations
 
@@ -26,6 +36,34 @@ from .qwen3 import Qwen3ForCausalLM, load_safetensors_dir
 from .sequence import Sequence
 
 DEFAULT_DECODE_GRAPH_BATCH_SIZES = [1, 2, 4, 8, 16, 32]
+
+
+class _TokenFetch:
+    """A pinned host copy of one step's greedy ids and the event that says it has landed."""
+
+    def __init__(self, n: int):
+        self.buf = torch.empty(n, dtype=torch.int64, pin_memory=True)
+        self.event = torch.cuda.Event()
+
+    def start(self, ids: torch.Tensor) -> "_TokenFetch":
+        self.buf.copy_(ids, non_blocking=True)
+        self.event.record()
+        return self
+
+    def tokens(self) -> list[int]:
+        self.event.synchronize()
+        return self.buf.tolist()
+
+
+class _InFlightStep:
+    """A decode step launched ahead of the call that asks for it."""
+
+    def __init__(self, slots, positions, entry, fetch: _TokenFetch, logits: torch.Tensor):
+        self.slots = slots
+        self.positions = positions
+        self.entry = entry
+        self.fetch = fetch
+        self.logits = logits
 
 
 class TokenIdTokenizer:
@@ -51,7 +89,8 @@ def _load_tokenizer(model_path, eos_token_id: int):
 class ModelRunner:
     def __init__(self, model_path, max_model_len: int, num_blocks: int | None, block_size: int, device_id: int,
                  npu_memory_utilization: float, enable_prefix_cache: bool = False, enable_decode_graph: bool = False,
-                 decode_graph_batch_sizes: list[int] | None = None, seed: int = 0, max_num_seqs: int = 64):
+                 decode_graph_batch_sizes: list[int] | None = None, seed: int = 0, max_num_seqs: int = 64,
+                 enable_overlap: bool = True):
         torch.cuda.set_device(device_id)
         self.device = torch.device("cuda", device_id)
         self.model_path = model_path
@@ -62,6 +101,12 @@ class ModelRunner:
         self.enable_prefix_cache = enable_prefix_cache
         self.enable_decode_graph = enable_decode_graph
         self.last_logits: torch.Tensor | None = None
+        self.enable_overlap = enable_overlap
+        self._in_flight: _InFlightStep | None = None
+        self._prefilled_since_decode = False
+        self._fetch: dict[int, list] = {}      # batch size -> [two _TokenFetch, next index]
+        self._logits_keep: dict[int, torch.Tensor] = {}
+        self.overlap_stats = {"launched": 0, "used": 0, "discarded": 0}
         self.config = load_config(model_path)
         self.tokenizer = _load_tokenizer(model_path, self.config.eos_token_id)
 
@@ -157,6 +202,7 @@ class ModelRunner:
     def prefill(self, seqs: list[Sequence]) -> None:
         if not seqs:
             return
+        self._prefilled_since_decode = True
         md = self.block_manager.prepare_prefill_metadata(
             slots=[s.seq_id for s in seqs], seq_lens=[s.runtime_prompt_len for s in seqs],
             start_positions=[s.cached_prefix_len for s in seqs], prefix_block_ids=[s.cached_block_ids for s in seqs],
@@ -171,6 +217,30 @@ class ModelRunner:
                                                      num_cached_blocks=len(seq.cached_block_ids),
                                                      num_full_blocks=seq.estimated_prompt_len // self.block_size)
 
+    def _fetch_tokens(self, b: int, ids: torch.Tensor) -> _TokenFetch:
+        slot = self._fetch.get(b)
+        if slot is None:
+            slot = self._fetch[b] = [_TokenFetch(b), _TokenFetch(b), 0]
+        f = slot[slot[2]]
+        slot[2] ^= 1  # ping-pong: the step launched ahead uses the other buffer
+        return f.start(ids)
+
+    def _keep_logits(self, b: int, logits: torch.Tensor) -> torch.Tensor:
+        """Copy a graph step's logits out of the static buffer the next replay overwrites."""
+        keep = self._logits_keep.get(b)
+        if keep is None or keep.shape != logits.shape:
+            keep = self._logits_keep[b] = torch.empty_like(logits)
+        keep.copy_(logits)
+        return keep
+
+    def _can_launch_ahead(self, seqs: list[Sequence]) -> bool:
+        # the next engine step decodes exactly these sequences when none finishes on a length
+        # limit or takes its final-token commit (engine.py), nothing was prefilled since the
+        # last decode (checked by the caller), and no EOS appears (unknown until the tokens are
+        # read: a miss is detected on the next call)
+        return self.enable_overlap and all(
+            seq.sampling_params.is_greedy() and len(seq.generated_token_ids) + 1 < seq.max_new_tokens for seq in seqs)
+
     @torch.inference_mode()
     def decode(self, seqs: list[Sequence]) -> None:
         if not seqs:
@@ -179,26 +249,47 @@ class ModelRunner:
         positions = [seq.cache_position for seq in seqs]
         slots = [seq.seq_id for seq in seqs]
         b = len(seqs)
-        logits = None
-        greedy_ids = None
         graph = self.decode_graph_runner
-        if graph is not None and graph.supports(b):
-            entry = graph.entry_for(b, 1, self.device, self.block_size)
-            md = self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens, width=entry.width,
-                                                            out=entry.buffers)
-            md = entry.metadata  # the static buffers now hold this step's inputs
-            logits = graph.replay(entry)
-            if logits is not None:
-                greedy_ids = entry.buffers["greedy_ids"]
+        ahead, self._in_flight = self._in_flight, None
+        entry = fetch = logits = None
+        if ahead is not None and ahead.slots == slots and ahead.positions == positions:
+            entry, fetch, logits = ahead.entry, ahead.fetch, ahead.logits  # launched by the previous call
+            self.overlap_stats["used"] += 1
         else:
-            if graph is not None:
-                graph.stats.fallbacks += 1
-            md = self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens)
-        if logits is None:
-            logits = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions, kv_cache=self.kv_cache,
-                                attn_metadata=md, is_prefill=False).logits
+            if ahead is not None:
+                self.overlap_stats["discarded"] += 1
+            if graph is not None and graph.supports(b):
+                entry = graph.entry_for(b, 1, self.device, self.block_size)
+                self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens, width=entry.width,
+                                                           out=entry.buffers)
+                logits = graph.replay(entry)  # the static buffers now hold this step's inputs
+                if logits is None:
+                    entry = None
+            else:
+                if graph is not None:
+                    graph.stats.fallbacks += 1
+            if entry is None:
+                md = self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens)
+                logits = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions,
+                                    kv_cache=self.kv_cache, attn_metadata=md, is_prefill=False).logits
+            elif all(seq.sampling_params.is_greedy() for seq in seqs):
+                fetch = self._fetch_tokens(b, entry.buffers["greedy_ids"])
+        self._prefilled_since_decode, prefilled = False, self._prefilled_since_decode
+        if entry is not None and fetch is not None and self._can_launch_ahead(seqs) and not prefilled:
+            # launch step N+1 behind this one: same sequences, next positions, input ids = this
+            # step's argmax (device to device); this step's logits leave the static buffer first
+            logits = self._keep_logits(b, logits)
+            nxt = [p + 1 for p in positions]
+            self.block_manager.prepare_decode_metadata(slots, nxt, 1, token_ids=tokens, width=entry.width,
+                                                       out=entry.buffers)
+            entry.buffers["input_ids"].copy_(entry.buffers["greedy_ids"])
+            nxt_logits = graph.replay(entry)
+            self._in_flight = _InFlightStep(slots, nxt, entry, self._fetch_tokens(b, entry.buffers["greedy_ids"]),
+                                            nxt_logits)
+            self.overlap_stats["launched"] += 1
         self.last_logits = logits
-        for seq, token in zip(seqs, self._sample(logits, seqs, greedy_ids)):
+        ids = fetch.tokens() if fetch is not None else self._sample(logits, seqs)
+        for seq, token in zip(seqs, ids):
             seq.set_decode_result(token)
 
     def decode_graph_stats(self) -> dict[str, int]:

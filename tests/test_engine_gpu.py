@@ -163,3 +163,36 @@ def test_fused_decode_path_matches_unfused_chain(device):
     print(f"fused vs unfused decode: {steps} steps compared, worst logit diff {worst:.4f}")
     assert fused.runner.model._gemm_workspace is not None and plain.runner.model._gemm_workspace is None
     assert steps >= 4 and worst <= 0.05
+
+
+@pytest.mark.gpu
+def test_overlapped_decode_equals_synchronous_loop(device):
+    """Launching step N+1 before step N's tokens reach the host changes nothing observable: the
+    same tokens (including a request that stops on EOS mid-run, which discards the step launched
+    ahead), and the per-step logits the runner exposes are those of the step just taken."""
+    prompts = prompts_for([20, 129, 64, 300], seed=5)
+    budgets = [7, 19, 13, 25]
+
+    def run(overlap, eos=-1):
+        llm = make_llm(graph=True)
+        llm.runner.enable_overlap = overlap
+        llm.runner.tokenizer.eos_token_id = eos
+        ids = [llm.submit(p, max_new_tokens=n) for p, n in zip(prompts, budgets)]
+        res, logits = {}, []
+        while llm.has_unfinished():
+            for o in llm.step():
+                res[o["request_id"]] = o["token_ids"]
+            if llm.runner.last_logits is not None:
+                logits.append(llm.runner.last_logits.float().cpu().clone())
+        return [res[i] for i in ids], logits, dict(llm.runner.overlap_stats)
+
+    sync_tokens, sync_logits, sync_stats = run(False)
+    tokens, logits, stats = run(True)
+    assert tokens == sync_tokens
+    assert len(logits) == len(sync_logits) and all(torch.equal(a, b) for a, b in zip(logits, sync_logits))
+    assert sync_stats["launched"] == 0 and stats["launched"] > 0 and stats["used"] > 0
+    # an EOS that the host only learns after the next step was launched: the launch is discarded
+    eos = sync_tokens[3][20]  # late in the longest request, when a step has been launched ahead
+    eos_sync, _, _ = run(False, eos=eos)
+    eos_tokens, _, eos_stats = run(True, eos=eos)
+    assert eos_tokens == eos_sync and eos_stats["discarded"] > 0
