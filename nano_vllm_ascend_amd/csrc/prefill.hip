@@ -8,8 +8,9 @@
 //          queries are the last q_len positions of kv_len, and query row r
 //          sees keys 0..kv_len-q_len+r (bottom-right causal; prefix-hit route).
 //
-// Workgroup = 4 waves = one kv head g, its GQA query heads, and a tile of
-// BQ = 128/GQA query tokens; wave w owns 32 query rows of one head.
+// Workgroup = 8 waves (two per SIMD, so one wave's softmax and LDS traffic
+// overlap the other's MFMAs) = one kv head g, its GQA query heads, and a tile
+// of BQ = 256/GQA query tokens; wave w owns 32 query rows of one head.
 // Per 64-key tile:
 //   S^T[64 keys x 32 queries] = K . Q^T  with v_mfma_f32_32x32x16_bf16
 //        (A = K rows from LDS, B = Q rows kept in registers for the whole loop).
@@ -19,10 +20,15 @@
 //        The contraction index can be permuted as long as both operands agree:
 //        taking the k-slots in the order the S^T accumulator already holds its
 //        rows makes P^T a register-only repack (no lane movement); V^T is read
-//        from a transposed LDS copy with two 8-byte reads per operand.
+//        from a transposed LDS copy whose keys are stored in that order, one
+//        16-byte read per operand.
+// Softmax: the running max is kept on raw scores and applied in the exponent's
+// FMA; its reference moves only when a score exceeds it by 2^8 (lazy rescale),
+// and the row sum adds each packed bf16 pair with one v_dot2.
 // Query tiles with the most keys dispatch first (tile index is the slowest
-// grid dimension, reversed); K/V of the next tile are loaded into registers
-// while the current tile's MFMAs run.
+// grid dimension, reversed).  K/V tiles are double-buffered in LDS: the next
+// tile is loaded into registers while the current one's MFMAs run, then
+// stored into the other slot, so each 64-key tile costs one barrier.
 #include "common.h"
 
 namespace nvamd {
@@ -30,7 +36,14 @@ namespace {
 
 constexpr int kBK = 64;            // keys per tile
 constexpr int kKStride = 136;      // LDS row stride (elements) of the K tile: 272 B, spreads banks
-constexpr int kVtStride = 68;      // LDS row stride (elements) of the transposed V tile: 34 dwords
+constexpr int kVtStride = 72;      // LDS row stride (elements) of the transposed V tile: 144 B, 16-byte aligned
+constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
+constexpr u32 kBf16PairOne = 0x3F803F80u;  // (1.0, 1.0) as a bf16 pair
+
+// Position of key k of a 64-key tile inside a V^T row.  Within each 16-key group the PV
+// step of lane half h consumes keys {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1); swapping
+// bits 2 and 3 of the key makes each of those sets 8 contiguous elements.
+__device__ __forceinline__ int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 struct PrefillArgs {
   u16 *out;
@@ -59,12 +72,15 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8v a, bf16x8v b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+
 template <int GQA, bool PAGED>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_kernel(PrefillArgs a) {
   constexpr int D = kHeadDim;
-  constexpr int BQ = 128 / GQA;     // query tokens per workgroup
-  constexpr int WPH = 4 / GQA;      // waves per query head
+  constexpr int BQ = 32 * kWaves / GQA;  // query tokens per workgroup
+  constexpr int WPH = kWaves / GQA;      // waves per query head
 
   const int g = blockIdx.x;
   const int s = blockIdx.y;
@@ -88,8 +104,8 @@ prefill_kernel(PrefillArgs a) {
   const bool q_ok = rq < q_len;
   const int64_t q_tok = q_start + min(rq, q_len - 1);
 
-  __shared__ __attribute__((aligned(16))) u16 sK[kBK][kKStride];
-  __shared__ __attribute__((aligned(16))) u16 sVt[D][kVtStride];
+  __shared__ __attribute__((aligned(16))) u16 sK[2][kBK][kKStride];
+  __shared__ __attribute__((aligned(16))) u16 sVt[2][D][kVtStride];
 
   // Q^T operand: lane holds dims 16kk + 8*hl + 0..7 of its query row, kk = 0..7.
   bf16x8v qf[8];
@@ -111,7 +127,7 @@ prefill_kernel(PrefillArgs a) {
   const int n_tiles = ceil_div(kv_hi, kBK);
   const int wave_last_key = offset + min(r0 + 31, q_len - 1);  // beyond: fully masked for this wave
 
-  // cooperative tile loads: K rows (t>>4)+16i, 16-byte chunk t&15; V row pair t&31, 16 dims (t>>5)
+  // cooperative tile loads: K rows (t>>4)+32i, 16-byte chunk t&15; V row pair t&31, 8 dims 8*(t>>5)
   const int kr = tid >> 4, kc = tid & 15;
   const int vp = tid & 31, vc = tid >> 5;
   const int32_t *bt_row = PAGED ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
@@ -127,116 +143,145 @@ prefill_kernel(PrefillArgs a) {
     return act + (int64_t)(q_start + key) * act_stride + (int64_t)g * D;
   };
 
-  u32x4 kreg[4], vreg[4];
-  auto load_tile = [&](int t) {
+  u32x4 kreg[2], vreg[2];
+  auto load_k = [&](int t) {
     const int base = t * kBK;
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = base + kr + 16 * i;
+    for (int i = 0; i < 2; ++i) {
+      const int key = base + kr + 32 * i;
       kreg[i] = key < kv_len ? ld16(row_ptr(a.k, a.k_stride, a.k_cache, key) + 8 * kc) : z;
     }
+  };
+  auto load_v = [&](int t) {
+    const int base = t * kBK;
+    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int key = base + 2 * vp + e;
-      const u16 *p = key < kv_len ? row_ptr(a.v, a.v_stride, a.v_cache, key) + 16 * vc : nullptr;
-      vreg[2 * e] = p ? ld16(p) : z;
-      vreg[2 * e + 1] = p ? ld16(p + 8) : z;
+      vreg[e] = key < kv_len ? ld16(row_ptr(a.v, a.v_stride, a.v_cache, key) + 8 * vc) : z;
     }
   };
-  auto store_tile = [&]() {
+  auto store_k = [&](int slot) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(&sK[kr + 16 * i][8 * kc]) = kreg[i];
-    // transpose V: (V[2vp][d], V[2vp+1][d]) -> one dword of row d of V^T
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const u32 a0 = vreg[half][e], a1 = vreg[2 + half][e];
-        const int d = 16 * vc + 8 * half + 2 * e;
-        *reinterpret_cast<u32 *>(&sVt[d][2 * vp]) = pair_lo(a0, a1);
-        *reinterpret_cast<u32 *>(&sVt[d + 1][2 * vp]) = pair_hi(a0, a1);
-      }
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4 *>(&sK[slot][kr + 32 * i][8 * kc]) = kreg[i];
   };
-
-  if (n_tiles > 0) load_tile(0);
-  for (int t = 0; t < n_tiles; ++t) {
-    __syncthreads();  // previous tile fully consumed
-    store_tile();
-    __syncthreads();
-    if (t + 1 < n_tiles) load_tile(t + 1);
-    const int base = t * kBK;
-    if (r0 >= q_len || base > wave_last_key) continue;  // nothing visible to this wave in this tile
-
-    // S^T = K Q^T for keys base..base+63 (two 32-key blocks)
-    f32x16 st[2];
+  auto store_v = [&](int slot) {
+    // transpose V: (V[2vp][d], V[2vp+1][d]) -> one dword of row d of V^T, at the permuted
+    // position of key 2vp (keys 2vp and 2vp+1 stay adjacent)
+    const int vpos = vt_pos(2 * vp);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = 8 * vc + 2 * e;
+      *reinterpret_cast<u32 *>(&sVt[slot][d][vpos]) = pair_lo(vreg[0][e], vreg[1][e]);
+      *reinterpret_cast<u32 *>(&sVt[slot][d + 1][vpos]) = pair_hi(vreg[0][e], vreg[1][e]);
+    }
+  };
+  // S^T = K Q^T for the 64 keys of a K slot (two 32-key blocks)
+  auto score = [&](int slot, f32x16 (&st)[2]) {
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) st[blk][i] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8v kf = *reinterpret_cast<const bf16x8v *>(&sK[32 * blk + n][16 * kk + 8 * hl]);
+        const bf16x8v kf = *reinterpret_cast<const bf16x8v *>(&sK[slot][32 * blk + n][16 * kk + 8 * hl]);
         st[blk] = mfma32(kf, qf[kk], st[blk]);
       }
     }
-    // scale + mask; key of register i of block blk: base + 32blk + 8(i/4) + 4hl + i%4
-    const bool need_mask = (base + kBK - 1 > offset + r0) || (base + kBK > kv_len);
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = st[blk][i] * a.scale_log2e;
-        if (need_mask) {
-          const int key = base + 32 * blk + 8 * (i / 4) + 4 * hl + (i % 4);
-          if (key > offset + rq || key >= kv_len) x = -INFINITY;
-        }
-        st[blk][i] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float ref = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - ref);
-    m_run = m_new;
-    float psum = 0.f;
-    bf16x8v pf[2][2];
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        u32x4 packed;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const u32 pr = pack_bf16x2(__builtin_amdgcn_exp2f(st[blk][8 * hh + 2 * e] - ref),
-                                     __builtin_amdgcn_exp2f(st[blk][8 * hh + 2 * e + 1] - ref));
-          psum += bf16_lo(pr) + bf16_hi(pr);
-          packed[e] = pr;
-        }
-        pf[blk][hh] = __builtin_bit_cast(bf16x8v, packed);
-      }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+  };
+  auto visible = [&](int t) { return r0 < q_len && t < n_tiles && t * kBK <= wave_last_key; };
 
-    // O^T += V^T P^T; k-slot 8hl+e of step (blk, hh) is key 32blk + 16hh + 8(e/4) + 4hl + e%4
+  // Double-buffered tiles: the next tile's K/V are loaded into registers while this tile's
+  // MFMAs run, then stored into the other LDS slot; one barrier per tile.
+  if (n_tiles > 0) {
+    load_k(0);
+    load_v(0);
+    store_k(0);
+    store_v(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 1 < n_tiles) {
+      load_k(t + 1);
+      load_v(t + 1);
+    }
+    const int base = t * kBK;
+    if (visible(t)) {
+      f32x16 st[2];
+      score(t & 1, st);
+      // mask; key of register i of block blk: base + 32blk + 8(i/4) + 4hl + i%4.  The running
+      // max is taken on raw scores (scale > 0) and applied in the exponent's FMA.
+      const bool need_mask = (base + kBK - 1 > offset + r0) || (base + kBK > kv_len);
+      const int key_lim = min(offset + rq, kv_len - 1);  // last key this lane's query row sees
+      float tmax = -INFINITY;
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
+      for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int k0 = 32 * blk + 16 * hh + 4 * hl;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const u16 *vrow = &sVt[32 * db + n][0];
-          const u32x2 lo = *reinterpret_cast<const u32x2 *>(vrow + k0);
-          const u32x2 hi = *reinterpret_cast<const u32x2 *>(vrow + k0 + 8);
-          const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
-          acc[db] = mfma32(__builtin_bit_cast(bf16x8v, vv), pf[blk][hh], acc[db]);
+        for (int i = 0; i < 16; ++i) {
+          float x = st[blk][i];
+          if (need_mask) {  // wave-uniform; the per-element test is a select
+            const int key = base + 32 * blk + 8 * (i / 4) + 4 * hl + (i % 4);
+            x = key <= key_lim ? x : -INFINITY;
+          }
+          st[blk][i] = x;
+          tmax = fmaxf(tmax, x);
         }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.scale_log2e;
+      // Lazy rescale: the exponent's reference moves only when a score exceeds it by more
+      // than 2^8, so P <= 256 and O, l are rescaled only on the tiles where some lane's
+      // reference moved.  O / l is unchanged by the choice of reference.
+      float alpha = 1.f;
+      if (tmax > m_run + kRescaleLog2) {
+        alpha = __builtin_amdgcn_exp2f(m_run - tmax);  // 0 on the first visible tile
+        m_run = tmax;
       }
+      const float neg_ref = m_run == -INFINITY ? 0.f : -m_run;
+      float psum = 0.f;
+      bf16x8v pf[2][2];
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          u32x4 packed;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const u32 pr =
+                pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(st[blk][8 * hh + 2 * e], a.scale_log2e, neg_ref)),
+                            __builtin_amdgcn_exp2f(fmaf(st[blk][8 * hh + 2 * e + 1], a.scale_log2e, neg_ref)));
+            psum = dot2_bf16(pr, kBf16PairOne, psum);  // both rounded values of the pair
+            packed[e] = pr;
+          }
+          pf[blk][hh] = __builtin_bit_cast(bf16x8v, packed);
+        }
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {  // wave-uniform
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+      }
+      l_run += psum;
+
+      // O^T += V^T P^T; k-slot 8hl+e of step (blk, hh) is key 32blk + 16hh + 8(e/4) + 4hl + e%4,
+      // which the permuted V^T layout stores contiguously: one 16-byte read per operand.
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int k0 = 32 * blk + 16 * hh + 8 * hl;
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            const u32x4 vv = *reinterpret_cast<const u32x4 *>(&sVt[t & 1][32 * db + n][k0]);
+            acc[db] = mfma32(__builtin_bit_cast(bf16x8v, vv), pf[blk][hh], acc[db]);
+          }
+        }
+    }
+    if (t + 1 < n_tiles) {  // nobody reads that slot: every wave finished tile t-1 before the last barrier
+      store_k((t + 1) & 1);
+      store_v((t + 1) & 1);
+    }
+    __syncthreads();
   }
 
   // normalise and write: register i of block db is dim 32db + 8(i/4) + 4hl + i%4 of query column n
@@ -258,16 +303,16 @@ prefill_kernel(PrefillArgs a) {
 template <int GQA, bool PAGED>
 int launch(const PrefillArgs &a, int n_seqs, hipStream_t stream) {
   dim3 grid(a.num_kv_heads, n_seqs, a.max_q_tiles);
-  hipLaunchKernelGGL((prefill_kernel<GQA, PAGED>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((prefill_kernel<GQA, PAGED>), grid, dim3(kThreads), 0, stream, a);
   return launch_status();
 }
 
 template <bool PAGED>
 int dispatch(PrefillArgs a, int n_seqs, int gqa, int max_q_len, hipStream_t stream) {
   switch (gqa) {
-    case 1: a.max_q_tiles = ceil_div(max_q_len, 128); return launch<1, PAGED>(a, n_seqs, stream);
-    case 2: a.max_q_tiles = ceil_div(max_q_len, 64); return launch<2, PAGED>(a, n_seqs, stream);
-    case 4: a.max_q_tiles = ceil_div(max_q_len, 32); return launch<4, PAGED>(a, n_seqs, stream);
+    case 1: a.max_q_tiles = ceil_div(max_q_len, 32 * kWaves); return launch<1, PAGED>(a, n_seqs, stream);
+    case 2: a.max_q_tiles = ceil_div(max_q_len, 16 * kWaves); return launch<2, PAGED>(a, n_seqs, stream);
+    case 4: a.max_q_tiles = ceil_div(max_q_len, 8 * kWaves); return launch<4, PAGED>(a, n_seqs, stream);
     default: return NVAMD_EUNSUPPORTED;
   }
 }
@@ -290,6 +335,7 @@ extern "C" int nvamd_varlen_prefill(void *out, int64_t out_stride, const void *q
                                     float scale, hipStream_t stream) {
   if (n_seqs == 0 || max_q_len == 0) return NVAMD_OK;
   if (head_dim != kHeadDim) return NVAMD_EUNSUPPORTED;
+  if (!(scale > 0.f)) return NVAMD_EINVAL;  // the softmax keeps its running max on raw scores
   if (!check_common(out, out_stride, q, q_stride, num_heads, num_kv_heads) || !k || !v || !cu_seqlens_q ||
       n_seqs < 0 || max_q_len < 0 || !aligned16(k) || !aligned16(v) || k_stride % 8 || v_stride % 8 ||
       k_stride < (int64_t)num_kv_heads * head_dim || v_stride < (int64_t)num_kv_heads * head_dim || n_seqs > 65535)
@@ -318,6 +364,7 @@ extern "C" int nvamd_paged_prefill(void *out, int64_t out_stride, const void *q,
   if (head_dim != kHeadDim) return NVAMD_EUNSUPPORTED;
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return NVAMD_EUNSUPPORTED;
+  if (!(scale > 0.f)) return NVAMD_EINVAL;  // the softmax keeps its running max on raw scores
   if (!check_common(out, out_stride, q, q_stride, num_heads, num_kv_heads) || !k_cache || !v_cache ||
       !block_tables || !cu_seqlens_q || !kv_lens || n_seqs < 0 || max_q_len < 0 || num_blocks <= 0 ||
       bt_width <= 0 || bt_stride < bt_width || !aligned16(k_cache) || !aligned16(v_cache) || n_seqs > 65535)
