@@ -11,9 +11,10 @@ them.  Inputs are resident in HBM before the timed region.
 
 Also reported: the roofline of the decode kernel (average launch duration from
 HIP events on the launch stream), the fp32 CPU oracle on the host cores as the
-CPU baseline, and (unless --no-e2e) the end-to-end output tok/s of the
-32 x 256-in / 2048-out greedy workload next to the reference's published
-910B3 figure.
+CPU baseline, the ragged causal prefill of 32 prompts of U[64, 2048] tokens
+(TFLOP/s against the dense bf16 MFMA peak) with its paged KV store (GB/s), and
+(unless --no-e2e) the end-to-end output tok/s of the 32 x 256-in / 2048-out
+greedy workload next to the reference's published 910B3 figure.
 """
 from __future__ import annotations
 
@@ -29,6 +30,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 REFERENCE_E2E_TOK_S = 1296.05  # nano_vllm_ascend on Ascend 910B3, 32 x 256/2048, bench_outputs/nano_32x256_2048.json
 NUM_LAYERS = 28
 
@@ -41,6 +43,7 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work budget of the baseline sample")
     ap.add_argument("--e2e-prompts", type=int, default=32)
     ap.add_argument("--e2e-input", type=int, default=256)
@@ -126,6 +129,57 @@ def decode_leg(args, device):
         "achieved": achieved,
         "work": work,
         "max_ctx": max_ctx,
+    }
+
+
+def prefill_leg(args, device) -> dict:
+    """Ragged causal prefill: 32 prompts of U[64, 2048] tokens packed with cu_seqlens, 16 q / 8 kv
+    heads, head_dim 128, bf16 N(0, 1); the K/V store into block_size-128 pages through a seeded
+    slot mapping, then varlen attention.  Timed with HIP events over repeated launches."""
+    import torch
+
+    from nano_vllm_ascend_amd import _C
+    from nano_vllm_ascend_amd import workloads as W
+
+    lens = W.prefill_lengths(32, 64, 2048, seed=args.seed)
+    t = sum(lens)
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    q = torch.randn(t, 16, 128, generator=gen, device=device).bfloat16()
+    k = torch.randn(t, 8, 128, generator=gen, device=device).bfloat16()
+    v = torch.randn(t, 8, 128, generator=gen, device=device).bfloat16()
+    cu = torch.tensor(W.cu_seqlens(lens), dtype=torch.int32, device=device)
+    out = torch.empty_like(q)
+    num_blocks = -(-t // 128) + 64
+    kc = torch.zeros(num_blocks, 128, 8, 128, dtype=torch.bfloat16, device=device)
+    vc = torch.zeros_like(kc)
+    slots = torch.randperm(num_blocks * 128, generator=torch.Generator().manual_seed(args.seed))[:t].to(device)
+    scale = 128 ** -0.5
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    us_attn = timed(lambda: _C.varlen_prefill(out, q, k, v, cu, max(lens), scale), 20)
+    us_store = timed(lambda: _C.kv_cache_write(k, v, kc, vc, slots), 20)
+    flops = W.causal_attention_flops(lens, lens, 16)
+    store_bytes = t * 8 * 128 * 2 * 2 * 2 + t * 8  # K and V read + written, slot ids
+    tflops = flops / us_attn / 1e6
+    return {
+        "workload": "ragged causal prefill, 32 prompts U[64, 2048] (seed %d), 16 q / 8 kv heads, d 128" % args.seed,
+        "tokens": t,
+        "attention": {"kernel": "prefill_kernel", "us": round(us_attn, 2), "flops": flops,
+                      "tflops": round(tflops, 1), "bound": "mfma", "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                      "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "kv_store": {"kernel": "kv_cache_write_kernel", "us": round(us_store, 2), "bytes": store_bytes,
+                     "gbs": round(store_bytes / us_store / 1e3, 1), "frac": round(store_bytes / us_store / 1e3 / HBM_PEAK_GBS, 4)},
     }
 
 
@@ -234,6 +288,9 @@ def main():
         result["cpu_baseline"] = cpu_baseline(dec["work"], args.cpu_seconds)
     del dec
     torch.cuda.empty_cache()
+    if not args.no_prefill:
+        result["prefill"] = prefill_leg(args, device)
+        torch.cuda.empty_cache()
     if not args.no_e2e:
         try:
             from nano_vllm_ascend_amd.bench_e2e import run_e2e

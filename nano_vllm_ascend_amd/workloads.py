@@ -144,6 +144,15 @@ def prefill_lengths(num_seqs: int = 32, lo: int = 64, hi: int = 2048, seed: int 
     return [rng.randint(lo, hi) for _ in range(num_seqs)]
 
 
+def causal_attention_flops(q_lens, kv_lens, num_heads: int, head_dim: int = 128) -> float:
+    """Algorithmic FLOPs of causal (bottom-right) attention: 4 * head_dim * num_heads per visible
+    (query, key) pair, QK^T and PV; query row r of a sequence sees kv_len - q_len + r + 1 keys."""
+    pairs = 0
+    for ql, kl in zip(q_lens, kv_lens):
+        pairs += ql * (kl - ql) + ql * (ql + 1) // 2
+    return 4.0 * head_dim * num_heads * pairs
+
+
 def cu_seqlens(lengths: list[int]) -> list[int]:
     out = [0]
     for n in lengths:

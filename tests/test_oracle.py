@@ -247,3 +247,13 @@ def test_planted_rotate_half_sign_error_is_caught(monkeypatch):
     monkeypatch.setattr(A, "rope_ref", wrong_rope)
     with pytest.raises(AssertionError):
         test_qk_norm_rope_matches_hf_layers()
+
+
+def test_product_flop_count_matches_oracle_and_brute_force():
+    """The benchmark's FLOP formula (package) equals the oracle's and a brute-force pair count."""
+    from nano_vllm_ascend_amd.workloads import causal_attention_flops
+    from oracle.attention_ref import prefill_flops
+
+    q_lens, kv_lens = [5, 1, 7, 3], [5, 9, 7, 11]
+    pairs = sum(1 for ql, kl in zip(q_lens, kv_lens) for r in range(ql) for j in range(kl) if j <= kl - ql + r)
+    assert causal_attention_flops(q_lens, kv_lens, 16) == prefill_flops(q_lens, kv_lens, 16) == 4 * 128 * 16 * pairs
