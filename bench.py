@@ -111,12 +111,16 @@ def decode_leg(args, device):
     # same kernel, so region time / launches is the kernel's average launch duration
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     start.record(stream)
-    for _ in range(args.steps):
+    marks[0].record(stream)
+    for i in range(args.steps):
         step()
+        marks[i + 1].record(stream)
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
+    step_ms = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
     launches = args.steps * NUM_LAYERS
     avg_launch_s = total_ms / 1e3 / launches
     value = bytes_per_launch * launches / (total_ms / 1e3) / 1e9
@@ -126,9 +130,66 @@ def decode_leg(args, device):
         "ms_per_step": total_ms / args.steps,
         "bytes_per_launch": bytes_per_launch,
         "avg_launch_us": avg_launch_s * 1e6,
+        "median_launch_us": step_ms[len(step_ms) // 2] * 1e3 / NUM_LAYERS,
         "achieved": achieved,
         "work": work,
         "max_ctx": max_ctx,
+    }
+
+
+def small_decode_leg(args, device) -> dict:
+    """Single-layer decode shape of 4 sequences, context U[1, 512], 64-block pools: as 28 launches
+    (one per layer, each its own pool, 0.9 GB in total) captured in one hipGraph, and as one eager
+    launch, which is latency-bound.  Medians over 50 replays / launches after 5 warm-ups."""
+    import torch
+
+    from nano_vllm_ascend_amd import _C
+    from nano_vllm_ascend_amd import workloads as W
+
+    work = W.make_decode(4, 1, 512, 64, args.seed, device, num_layers=NUM_LAYERS)
+    b = len(work.context_lens_list)
+    max_ctx = 512
+    scale = W.HEAD_DIM ** -0.5
+    ws = _C.alloc_paged_decode_workspace(b, W.NUM_HEADS, W.NUM_KV_HEADS, max_ctx, device)
+    out = torch.empty_like(work.q)
+    nbytes = (sum(work.context_lens_list) * W.NUM_KV_HEADS * W.HEAD_DIM * 2 * 2 + 2 * b * W.NUM_HEADS * W.HEAD_DIM * 2
+              + b * work.block_tables.shape[1] * 4 + b * 4)
+
+    def launch(layer):
+        _C.paged_decode(out, work.q, work.key_cache[layer], work.value_cache[layer], work.block_tables,
+                        work.context_lens, scale, max_ctx, ws)
+
+    for layer in range(NUM_LAYERS):  # eager warm-up outside the capture
+        launch(layer)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in range(NUM_LAYERS):
+            launch(layer)
+
+    def median_ms(fn, reps=50, warm=5):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        ev[0].record()
+        for i in range(reps):
+            fn()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        t = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+        return t[len(t) // 2]
+
+    graph_us = median_ms(graph.replay) * 1e3 / NUM_LAYERS
+    single_us = median_ms(lambda: launch(0)) * 1e3
+    return {
+        "workload": "decode 4 seqs, context U[1, 512] (sum %d), 64-block pools" % sum(work.context_lens_list),
+        "bytes_per_launch": nbytes,
+        "graph_28_layers": {"us_per_launch": round(graph_us, 3), "gbs": round(nbytes / graph_us / 1e3, 1),
+                            "frac": round(nbytes / graph_us / 1e3 / HBM_PEAK_GBS, 4)},
+        "single_launch": {"us": round(single_us, 3), "gbs": round(nbytes / single_us / 1e3, 1),
+                          "note": "latency-bound: one small launch"},
+        "work": work,
     }
 
 
@@ -226,6 +287,50 @@ def cpu_baseline(work, seconds: float):
     }
 
 
+def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 2) -> dict:
+    """fp32 oracle on the host cores for the other decode shape (median of 20 reps after 3
+    warm-ups) and for the ragged prefill (a bounded sample of `prefill_reps` reps)."""
+    import torch
+
+    from nano_vllm_ascend_amd import workloads as W
+    from oracle.attention_ref import paged_decode_ref, varlen_prefill_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = small_work
+    q, kc, vc = w.q.cpu(), w.key_cache[0].cpu(), w.value_cache[0].cpu()
+    bt, ctx = w.block_tables.cpu(), w.context_lens.cpu()
+    scale = 128 ** -0.5
+    for _ in range(3):
+        paged_decode_ref(q, kc, vc, bt, ctx, scale)
+    times = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        paged_decode_ref(q, kc, vc, bt, ctx, scale)
+        times.append(time.perf_counter() - t0)
+    dec_s = sorted(times)[10]
+    nbytes = sum(w.context_lens_list) * 8 * 128 * 4 + 2 * 4 * 16 * 128 * 2
+    lens = W.prefill_lengths(32, 64, 2048, seed=seed)
+    t = sum(lens)
+    g = torch.Generator().manual_seed(seed)
+    pq = torch.randn(t, 16, 128, generator=g).bfloat16()
+    pk = torch.randn(t, 8, 128, generator=g).bfloat16()
+    pv = torch.randn(t, 8, 128, generator=g).bfloat16()
+    cu = torch.tensor(W.cu_seqlens(lens), dtype=torch.int32)
+    t0 = time.perf_counter()
+    for _ in range(prefill_reps):
+        varlen_prefill_ref(pq, pk, pv, cu, scale)
+    pf_s = (time.perf_counter() - t0) / prefill_reps
+    return {
+        "cores": cores, "kind": "port",
+        "decode_4seq": {"us": round(dec_s * 1e6, 1), "gbs": round(nbytes / dec_s / 1e9, 2),
+                        "sample": "fp32 torch-CPU oracle, layer 0, median of 20 after 3 warm-ups"},
+        "prefill_32xU64-2048": {"ms": round(pf_s * 1e3, 1),
+                                "tflops": round(W.causal_attention_flops(lens, lens, 16) / pf_s / 1e12, 3),
+                                "sample": f"fp32 torch-CPU oracle, {prefill_reps} reps (bounded sample)"},
+    }
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -282,11 +387,15 @@ def main():
             "traffic": traffic,
             "bytes_per_launch": dec["bytes_per_launch"],
             "avg_launch_us": round(dec["avg_launch_us"], 3),
+            "median_launch_us": round(dec["median_launch_us"], 3),
         },
     }
+    small = small_decode_leg(args, device)
+    result["decode_small"] = {k: v for k, v in small.items() if k != "work"}
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(dec["work"], args.cpu_seconds)
-    del dec
+        result["cpu_baseline_other"] = cpu_baselines_other(small["work"], args.seed)
+    del dec, small
     torch.cuda.empty_cache()
     if not args.no_prefill:
         result["prefill"] = prefill_leg(args, device)
