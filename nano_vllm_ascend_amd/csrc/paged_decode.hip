@@ -29,8 +29,8 @@
 // Merge: each wave folds its 8 row groups with DPP and swizzles, wave 0 folds the
 // NW waves through LDS.  A multi-partition unit's wave 0 then publishes
 // (max, sum, acc[128]) per head with agent-scope write-through stores, waits for
-// them, and bumps an arrival counter; the last to arrive reads every partial with
-// one round of agent-scope loads and writes the output.  No L2 writeback or
+// them, and bumps an arrival counter; the last to arrive reads the partials with
+// agent-scope loads, all issued before the first is used, and writes the output.  No L2 writeback or
 // invalidate is needed.
 #include "common.h"
 
@@ -88,6 +88,11 @@ __device__ __forceinline__ void store_agent2(float *p, float lo, float hi) {
   const uint64_t v = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
   __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Raw buffer resource word 3 for gfx9 (32-bit data, no format conversion), and the cache
+// policy of an agent-coherent load (sc1), as the agent-scope atomic loads below use.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kCachePolicyAgent = 16;
+
 __device__ __forceinline__ void load_agent2(const float *p, float &lo, float &hi) {
   const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(p)), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -366,21 +371,47 @@ paged_decode_kernel(DecodeArgs a) {
   prev = __shfl(prev, 0);
   if (prev != n_parts - 1) return;
 
-  // Merge.  Lane x holds partition x's (max, sum) of every head (one round of loads),
-  // then the accumulators arrive 8 partitions per round, all loads issued before use.
-  float fx[GQA], den[GQA];
+  // Merge.  Lane x holds partition x's (max, sum) of every head; the accumulators of the
+  // first MP partitions are loaded in the same round (every load issued before the first
+  // use, so the merge waits for one memory round trip), later ones 8 partitions per round.
+  // The first round uses buffer loads over exactly the n_parts published partitions: the
+  // range check returns zeros past them without a branch or a memory access.
+  constexpr int MP = GQA <= 2 ? 16 : 8;
+  const __amdgpu_buffer_rsrc_t parts_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      part_base, 0, n_parts * GQA * kPartFloats * (int)sizeof(float), kBufferRsrcWord3);
+  float pm[GQA], pl[GQA], v0f[GQA][MP], v1f[GQA][MP];
 #pragma unroll
   for (int j = 0; j < GQA; ++j) {
-    float pm = -INFINITY, pl = 0.f;
-    if (lane < n_parts) load_agent2(part_base + ((int64_t)lane * GQA + j) * kPartFloats, pm, pl);
-    const float M = wave_max(pm);
-    fx[j] = pm == -INFINITY ? 0.f : fast_exp2(pm - M);
-    den[j] = wave_sum(fx[j] * pl);
+    const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(
+        parts_rsrc, (lane * GQA + j) * kPartFloats * (int)sizeof(float), 0, kCachePolicyAgent);
+    pm[j] = lane < n_parts ? __uint_as_float(ml[0]) : -INFINITY;
+    pl[j] = __uint_as_float(ml[1]);
   }
-  float n0[GQA], n1[GQA];
 #pragma unroll
-  for (int j = 0; j < GQA; ++j) n0[j] = n1[j] = 0.f;
-  for (int x0 = 0; x0 < n_parts; x0 += 8) {
+  for (int k = 0; k < MP; ++k) {
+#pragma unroll
+    for (int j = 0; j < GQA; ++j) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
+          parts_rsrc, ((k * GQA + j) * kPartFloats + 2 + 2 * lane) * (int)sizeof(float), 0, kCachePolicyAgent);
+      v0f[j][k] = __uint_as_float(v[0]);
+      v1f[j][k] = __uint_as_float(v[1]);
+    }
+  }
+  float fx[GQA], den[GQA], n0[GQA], n1[GQA];
+#pragma unroll
+  for (int j = 0; j < GQA; ++j) {
+    const float M = wave_max(pm[j]);
+    fx[j] = pm[j] == -INFINITY ? 0.f : fast_exp2(pm[j] - M);
+    den[j] = wave_sum(fx[j] * pl[j]);
+    n0[j] = n1[j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < MP; ++k) {  // partitions past n_parts load zeros and weigh 0
+      const float f = readlane(fx[j], k);
+      n0[j] += f * v0f[j][k];
+      n1[j] += f * v1f[j][k];
+    }
+  }
+  for (int x0 = MP; x0 < n_parts; x0 += 8) {
     float v0[GQA][8], v1[GQA][8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
