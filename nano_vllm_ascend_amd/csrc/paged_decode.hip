@@ -102,12 +102,13 @@ __device__ __forceinline__ void load_agent2(const float *p, float &lo, float &hi
 
 // GQA 1, and GQA 2 with one chunk per wave, fit 128 VGPRs without spills: four waves
 // per SIMD.
-template <int GQA, int NW, int CPW>
+template <int GQA, int NW, int CPW, int TILES>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((GQA == 1 || (GQA == 2 && CPW == 1)) ? 4 : 1)))
 paged_decode_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
-  constexpr int WT = CPW * 64;  // tokens per wave
+  constexpr int CT = 16 * TILES;  // tokens per chunk: TILES tiles of 16 rows
+  constexpr int WT = CPW * CT;    // tokens per wave
   constexpr int PART = NW * WT;
 
   const int hkv = a.num_kv_heads;
@@ -184,10 +185,10 @@ paged_decode_kernel(DecodeArgs a) {
   if (t_begin < t_end) {
     const int last_tile = (t_end - 1) & ~15;
 #pragma unroll 1
-    for (int tc = t_begin; tc < t_end; tc += 64) {
-      KVTile T[4];
+    for (int tc = t_begin; tc < t_end; tc += CT) {
+      KVTile T[TILES];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < TILES; ++i) {
         const int t0 = min(tc + 16 * i, last_tile);
         int blk = bt_row[t0 >> a.bs_log2];
         blk = min(max(blk, 0), a.num_blocks - 1);  // never leave the pool
@@ -206,9 +207,9 @@ paged_decode_kernel(DecodeArgs a) {
       }
 
       // QK for the chunk: s[tile][row a/b][head]
-      float s[4][2][GQA];
+      float s[TILES][2][GQA];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < TILES; ++i) {
 #pragma unroll
         for (int j = 0; j < GQA; ++j) {
           float sa = 0.f, sb = 0.f;
@@ -226,9 +227,9 @@ paged_decode_kernel(DecodeArgs a) {
           s[i][1][j] = sb;
         }
       }
-      bool ok[4][2];
+      bool ok[TILES][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < TILES; ++i) {
         ok[i][0] = (tc + 16 * i + r) < t_end;
         ok[i][1] = (tc + 16 * i + 8 + r) < t_end;
 #pragma unroll
@@ -241,18 +242,18 @@ paged_decode_kernel(DecodeArgs a) {
       }
 
       // Online softmax, one step per chunk, per 8-lane row group.
-      u32 pp[4][GQA];
+      u32 pp[TILES][GQA];
 #pragma unroll
       for (int j = 0; j < GQA; ++j) {
         float cm = m[j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cm = fmaxf(cm, fmaxf(s[i][0][j], s[i][1][j]));
+        for (int i = 0; i < TILES; ++i) cm = fmaxf(cm, fmaxf(s[i][0][j], s[i][1][j]));
         const float ref = cm == -INFINITY ? 0.f : cm;  // a group with no valid row yet
         const float alpha = fast_exp2(m[j] - ref);
         m[j] = cm;
         float add = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TILES; ++i) {
           pp[i][j] = pack_bf16x2(fast_exp2(s[i][0][j] - ref), fast_exp2(s[i][1][j] - ref));
           add += bf16_lo(pp[i][j]) + bf16_hi(pp[i][j]);
         }
@@ -262,16 +263,16 @@ paged_decode_kernel(DecodeArgs a) {
       }
 
       // Rows past the context may hold stale bits (NaN * 0 = NaN): zero their V.
-      if (tc + 64 > t_end) {
+      if (tc + CT > t_end) {
         const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TILES; ++i) {
           if (!ok[i][0]) { T[i].va0 = z; T[i].va1 = z; }
           if (!ok[i][1]) { T[i].vb0 = z; T[i].vb1 = z; }
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < TILES; ++i) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const u32 lo0 = pair_lo(T[i].va0[e], T[i].vb0[e]);
@@ -442,15 +443,15 @@ paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-template <int GQA, int NW, int CPW>
+template <int GQA, int NW, int CPW, int TILES = 4>
 int launch(DecodeArgs a, int batch, hipStream_t stream) {
-  constexpr int PART = NW * CPW * 64;
+  constexpr int PART = NW * CPW * 16 * TILES;
   a.max_parts = ceil_div(a.max_ctx, PART);
   if (a.max_parts > 64) return NVAMD_EUNSUPPORTED;  // merge stage holds <= 64 partitions
   a.batch = batch;
   // One workgroup per possible (b, g, p); the ones past the last existing item exit at once.
   dim3 grid((unsigned)((int64_t)batch * a.num_kv_heads * a.max_parts));
-  hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW>), grid, dim3(NW * 64), 0, stream, a);
+  hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW, TILES>), grid, dim3(NW * 64), 0, stream, a);
   return launch_status();
 }
 

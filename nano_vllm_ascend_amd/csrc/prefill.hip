@@ -8,9 +8,11 @@
 //          queries are the last q_len positions of kv_len, and query row r
 //          sees keys 0..kv_len-q_len+r (bottom-right causal; prefix-hit route).
 //
-// Workgroup = 8 waves (two per SIMD, so one wave's softmax and LDS traffic
-// overlap the other's MFMAs) = one kv head g, its GQA query heads, and a tile
-// of BQ = 256/GQA query tokens; wave w owns 32 query rows of one head.
+// Workgroup = 4 waves = one kv head g, its GQA query heads, and a tile of
+// BQ = 128/GQA query tokens; wave w owns 32 query rows of one head.  Two
+// workgroups share a CU (two waves per SIMD, 2 x 70 KB of LDS), so one wave's
+// softmax and LDS traffic overlap the other's MFMAs and the two workgroups'
+// per-tile barriers do not hold each other up.
 // Per 64-key tile:
 //   S^T[64 keys x 32 queries] = K . Q^T  with v_mfma_f32_32x32x16_bf16
 //        (A = K rows from LDS, B = Q rows kept in registers for the whole loop).
@@ -25,10 +27,14 @@
 // Softmax: the running max is kept on raw scores and applied in the exponent's
 // FMA; its reference moves only when a score exceeds it by 2^8 (lazy rescale),
 // and the row sum adds each packed bf16 pair with one v_dot2.
-// Query tiles with the most keys dispatch first (tile index is the slowest
-// grid dimension, reversed).  K/V tiles are double-buffered in LDS: the next
-// tile is loaded into registers while the current one's MFMAs run, then
-// stored into the other slot, so each 64-key tile costs one barrier.
+// Grid (kv head, query tile, sequence), dispatched in that order: with 8 kv heads the
+// hardware's round-robin over the 8 XCDs puts every query tile of one (sequence, kv
+// head) on one XCD, back to back, heaviest (most keys) first, so they read that head's
+// K/V tiles while the XCD's L2 still holds them (a query-tile-major order streams every
+// sequence's K/V from memory once per tile: 1.3x the time).  K/V tiles are
+// double-buffered in LDS: the next tile is loaded into registers while the current
+// one's MFMAs run, then stored into the other slot, so each 64-key tile costs one
+// barrier.
 #include "common.h"
 
 namespace nvamd {
@@ -72,8 +78,11 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8v a, bf16x8v b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;  // two workgroups per CU (LDS 2 x 70 KB): their barriers are independent
 constexpr int kThreads = kWaves * 64;
+constexpr int kKLoads = kBK * 16 / kThreads;      // 16-byte K chunks per thread per tile
+constexpr int kVLoads = kBK / 2 * 16 / kThreads;  // (key pair, 8-dim chunk) units per thread
+static_assert(kKLoads >= 1 && kVLoads >= 1, "tile staging needs <= 512 threads");
 
 template <int GQA, bool PAGED>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
@@ -83,8 +92,8 @@ prefill_kernel(PrefillArgs a) {
   constexpr int WPH = kWaves / GQA;      // waves per query head
 
   const int g = blockIdx.x;
-  const int s = blockIdx.y;
-  const int qt = a.max_q_tiles - 1 - (int)blockIdx.z;
+  const int qt = a.max_q_tiles - 1 - (int)blockIdx.y;
+  const int s = blockIdx.z;
   const int q_start = a.cu_seqlens_q[s];
   const int q_len = a.cu_seqlens_q[s + 1] - q_start;
   if (qt * BQ >= q_len) return;
@@ -127,7 +136,8 @@ prefill_kernel(PrefillArgs a) {
   const int n_tiles = ceil_div(kv_hi, kBK);
   const int wave_last_key = offset + min(r0 + 31, q_len - 1);  // beyond: fully masked for this wave
 
-  // cooperative tile loads: K rows (t>>4)+32i, 16-byte chunk t&15; V row pair t&31, 8 dims 8*(t>>5)
+  // cooperative tile loads: K rows (t>>4) + (threads/16)i, 16-byte chunk t&15; V row pair t&31,
+  // 8 dims 8 * ((t>>5) + (threads/32)e)
   const int kr = tid >> 4, kc = tid & 15;
   const int vp = tid & 31, vc = tid >> 5;
   const int32_t *bt_row = PAGED ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
@@ -143,39 +153,43 @@ prefill_kernel(PrefillArgs a) {
     return act + (int64_t)(q_start + key) * act_stride + (int64_t)g * D;
   };
 
-  u32x4 kreg[2], vreg[2];
+  // Keys past kv_len re-read the last key's row (a finite value): their scores are masked
+  // to -inf, so they enter P as exact zeros, and the loads need no branch.
+  u32x4 kreg[kKLoads], vreg[kVLoads][2];
   auto load_k = [&](int t) {
     const int base = t * kBK;
-    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int key = base + kr + 32 * i;
-      kreg[i] = key < kv_len ? ld16(row_ptr(a.k, a.k_stride, a.k_cache, key) + 8 * kc) : z;
+    for (int i = 0; i < kKLoads; ++i) {
+      const int key = min(base + kr + kThreads / 16 * i, kv_len - 1);
+      kreg[i] = ld16(row_ptr(a.k, a.k_stride, a.k_cache, key) + 8 * kc);
     }
   };
   auto load_v = [&](int t) {
     const int base = t * kBK;
-    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int key = base + 2 * vp + e;
-      vreg[e] = key < kv_len ? ld16(row_ptr(a.v, a.v_stride, a.v_cache, key) + 8 * vc) : z;
-    }
+    for (int i = 0; i < kVLoads; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int key = min(base + 2 * vp + e, kv_len - 1);
+        vreg[i][e] = ld16(row_ptr(a.v, a.v_stride, a.v_cache, key) + 8 * (vc + kThreads / 32 * i));
+      }
   };
   auto store_k = [&](int slot) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4 *>(&sK[slot][kr + 32 * i][8 * kc]) = kreg[i];
+    for (int i = 0; i < kKLoads; ++i) *reinterpret_cast<u32x4 *>(&sK[slot][kr + kThreads / 16 * i][8 * kc]) = kreg[i];
   };
   auto store_v = [&](int slot) {
     // transpose V: (V[2vp][d], V[2vp+1][d]) -> one dword of row d of V^T, at the permuted
     // position of key 2vp (keys 2vp and 2vp+1 stay adjacent)
     const int vpos = vt_pos(2 * vp);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int d = 8 * vc + 2 * e;
-      *reinterpret_cast<u32 *>(&sVt[slot][d][vpos]) = pair_lo(vreg[0][e], vreg[1][e]);
-      *reinterpret_cast<u32 *>(&sVt[slot][d + 1][vpos]) = pair_hi(vreg[0][e], vreg[1][e]);
-    }
+    for (int i = 0; i < kVLoads; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = 8 * (vc + kThreads / 32 * i) + 2 * e;
+        *reinterpret_cast<u32 *>(&sVt[slot][d][vpos]) = pair_lo(vreg[i][0][e], vreg[i][1][e]);
+        *reinterpret_cast<u32 *>(&sVt[slot][d + 1][vpos]) = pair_hi(vreg[i][0][e], vreg[i][1][e]);
+      }
   };
   // S^T = K Q^T for the 64 keys of a K slot (two 32-key blocks)
   auto score = [&](int slot, f32x16 (&st)[2]) {
@@ -212,21 +226,23 @@ prefill_kernel(PrefillArgs a) {
       score(t & 1, st);
       // mask; key of register i of block blk: base + 32blk + 8(i/4) + 4hl + i%4.  The running
       // max is taken on raw scores (scale > 0) and applied in the exponent's FMA.
+      // Only tiles that cross this wave's diagonal or the end of the keys need the mask
+      // (1-2 per wave); the test is wave-uniform, so the others skip it with one branch.
       const bool need_mask = (base + kBK - 1 > offset + r0) || (base + kBK > kv_len);
-      const int key_lim = min(offset + rq, kv_len - 1);  // last key this lane's query row sees
+      if (__builtin_expect(need_mask, 0)) {
+        // lane's last visible key, relative to the key of register 0 of block 0
+        const int lim = min(offset + rq, kv_len - 1) - base - 4 * hl;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (32 * blk + 8 * (i / 4) + (i % 4) > lim) st[blk][i] = -INFINITY;
+      }
       float tmax = -INFINITY;
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float x = st[blk][i];
-          if (need_mask) {  // wave-uniform; the per-element test is a select
-            const int key = base + 32 * blk + 8 * (i / 4) + 4 * hl + (i % 4);
-            x = key <= key_lim ? x : -INFINITY;
-          }
-          st[blk][i] = x;
-          tmax = fmaxf(tmax, x);
-        }
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[blk][i]);
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.scale_log2e;
       // Lazy rescale: the exponent's reference moves only when a score exceeds it by more
       // than 2^8, so P <= 256 and O, l are rescaled only on the tiles where some lane's
@@ -302,7 +318,7 @@ prefill_kernel(PrefillArgs a) {
 
 template <int GQA, bool PAGED>
 int launch(const PrefillArgs &a, int n_seqs, hipStream_t stream) {
-  dim3 grid(a.num_kv_heads, n_seqs, a.max_q_tiles);
+  dim3 grid(a.num_kv_heads, a.max_q_tiles, n_seqs);
   hipLaunchKernelGGL((prefill_kernel<GQA, PAGED>), grid, dim3(kThreads), 0, stream, a);
   return launch_status();
 }
