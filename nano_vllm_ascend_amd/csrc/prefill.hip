@@ -214,6 +214,12 @@ prefill_kernel(PrefillArgs a) {
     store_k(0);
     store_v(0);
   }
+  // Drain every load issued so far (the Q fragments) before the loop.  Otherwise the wait
+  // the compiler places ahead of the first use of Q is kept on every iteration, and each
+  // tile's MFMAs would wait for the next tile's K/V loads issued just before them.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
     if (t + 1 < n_tiles) {
