@@ -20,6 +20,12 @@ typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
 constexpr int kHeadDim = 128;
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Raw buffer resource word 3 for gfx9 (32-bit data, no format conversion).  A raw buffer
+// load whose byte offset is at or past num_records returns zeros without a memory access.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+// Cache policy of an agent-coherent buffer load (sc1), as agent-scope atomic loads use.
+constexpr int kCachePolicyAgent = 16;
+
 // bf16 <-> fp32.  A bf16 is the top half of an fp32, so widening is a shift.
 __device__ __forceinline__ float bf16_lo(u32 x) { return __uint_as_float(x << 16); }
 __device__ __forceinline__ float bf16_hi(u32 x) { return __uint_as_float(x & 0xffff0000u); }

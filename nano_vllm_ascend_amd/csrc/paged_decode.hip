@@ -88,10 +88,6 @@ __device__ __forceinline__ void store_agent2(float *p, float lo, float hi) {
   const uint64_t v = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
   __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Raw buffer resource word 3 for gfx9 (32-bit data, no format conversion), and the cache
-// policy of an agent-coherent load (sc1), as the agent-scope atomic loads below use.
-constexpr int kBufferRsrcWord3 = 0x00020000;
-constexpr int kCachePolicyAgent = 16;
 
 __device__ __forceinline__ void load_agent2(const float *p, float &lo, float &hi) {
   const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(p)), __ATOMIC_RELAXED,

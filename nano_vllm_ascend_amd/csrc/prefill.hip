@@ -44,6 +44,9 @@ constexpr int kBK = 64;            // keys per tile
 constexpr int kKStride = 136;      // LDS row stride (elements) of the K tile: 272 B, spreads banks
 constexpr int kVtStride = 72;      // LDS row stride (elements) of the transposed V tile: 144 B, 16-byte aligned
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
+// Largest K/V activation row stride (elements) of the dense route: a 64-row tile's byte range
+// is a 32-bit buffer size.
+constexpr int64_t kMaxActStride = (int64_t)1 << 24;
 constexpr u32 kBf16PairOne = 0x3F803F80u;  // (1.0, 1.0) as a bf16 pair
 
 // Position of key k of a 64-key tile inside a V^T row.  Within each 16-key group the PV
@@ -144,35 +147,62 @@ prefill_kernel(PrefillArgs a) {
   const int64_t cache_row = (int64_t)a.num_kv_heads * D;
   const int bs_mask = (1 << a.bs_log2) - 1;
 
-  auto row_ptr = [&](const u16 *act, int64_t act_stride, const u16 *cache, int key) -> const u16 * {
-    if (PAGED) {
-      int blk = bt_row[key >> a.bs_log2];
-      blk = min(max(blk, 0), a.num_blocks - 1);
-      return cache + (((int64_t)blk << a.bs_log2) + (key & bs_mask)) * cache_row + (int64_t)g * D;
-    }
-    return act + (int64_t)(q_start + key) * act_stride + (int64_t)g * D;
+  // Paged route: each row through the block table.  Keys past kv_len re-read the last key's
+  // row (a finite value): their scores are masked to -inf, so they enter P as exact zeros.
+  auto row_ptr = [&](const u16 *cache, int key) -> const u16 * {
+    key = min(key, kv_len - 1);
+    int blk = bt_row[key >> a.bs_log2];
+    blk = min(max(blk, 0), a.num_blocks - 1);
+    return cache + (((int64_t)blk << a.bs_log2) + (key & bs_mask)) * cache_row + (int64_t)g * D;
   };
-
-  // Keys past kv_len re-read the last key's row (a finite value): their scores are masked
-  // to -inf, so they enter P as exact zeros, and the loads need no branch.
-  u32x4 kreg[kKLoads], vreg[kVLoads][2];
-  auto load_k = [&](int t) {
-    const int base = t * kBK;
+  // Dense route: one raw buffer descriptor per tile over the tile's rows of this sequence
+  // (built in scalar registers); every thread's byte offsets inside a tile are constants and
+  // rows past kv_len read as zeros, so a load costs no vector address arithmetic.
+  u32 k_off[kKLoads], v_off[kVLoads][2];
+  if (!PAGED) {
 #pragma unroll
-    for (int i = 0; i < kKLoads; ++i) {
-      const int key = min(base + kr + kThreads / 16 * i, kv_len - 1);
-      kreg[i] = ld16(row_ptr(a.k, a.k_stride, a.k_cache, key) + 8 * kc);
-    }
-  };
-  auto load_v = [&](int t) {
-    const int base = t * kBK;
+    for (int i = 0; i < kKLoads; ++i)
+      k_off[i] = (u32)(((kr + kThreads / 16 * i) * a.k_stride + g * D + 8 * kc) * 2);
 #pragma unroll
     for (int i = 0; i < kVLoads; ++i)
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int key = min(base + 2 * vp + e, kv_len - 1);
-        vreg[i][e] = ld16(row_ptr(a.v, a.v_stride, a.v_cache, key) + 8 * (vc + kThreads / 32 * i));
-      }
+      for (int e = 0; e < 2; ++e)
+        v_off[i][e] = (u32)(((2 * vp + e) * a.v_stride + g * D + 8 * (vc + kThreads / 32 * i)) * 2);
+  }
+  auto tile_rsrc = [&](const u16 *act, int64_t stride, int t) {
+    const int base = t * kBK;
+    const int rows = min(kv_len - base, kBK);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<u16 *>(act + (int64_t)(q_start + base) * stride), 0,
+                                             rows * (int)stride * 2, kBufferRsrcWord3);
+  };
+
+  u32x4 kreg[kKLoads], vreg[kVLoads][2];
+  auto load_k = [&](int t) {
+    if (PAGED) {
+#pragma unroll
+      for (int i = 0; i < kKLoads; ++i) kreg[i] = ld16(row_ptr(a.k_cache, t * kBK + kr + kThreads / 16 * i) + 8 * kc);
+    } else {
+      const __amdgpu_buffer_rsrc_t r = tile_rsrc(a.k, a.k_stride, t);
+#pragma unroll
+      for (int i = 0; i < kKLoads; ++i)
+        kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, k_off[i], 0, 0));
+    }
+  };
+  auto load_v = [&](int t) {
+    if (PAGED) {
+#pragma unroll
+      for (int i = 0; i < kVLoads; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          vreg[i][e] = ld16(row_ptr(a.v_cache, t * kBK + 2 * vp + e) + 8 * (vc + kThreads / 32 * i));
+    } else {
+      const __amdgpu_buffer_rsrc_t r = tile_rsrc(a.v, a.v_stride, t);
+#pragma unroll
+      for (int i = 0; i < kVLoads; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          vreg[i][e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, v_off[i][e], 0, 0));
+    }
   };
   auto store_k = [&](int slot) {
 #pragma unroll
@@ -360,7 +390,8 @@ extern "C" int nvamd_varlen_prefill(void *out, int64_t out_stride, const void *q
   if (!(scale > 0.f)) return NVAMD_EINVAL;  // the softmax keeps its running max on raw scores
   if (!check_common(out, out_stride, q, q_stride, num_heads, num_kv_heads) || !k || !v || !cu_seqlens_q ||
       n_seqs < 0 || max_q_len < 0 || !aligned16(k) || !aligned16(v) || k_stride % 8 || v_stride % 8 ||
-      k_stride < (int64_t)num_kv_heads * head_dim || v_stride < (int64_t)num_kv_heads * head_dim || n_seqs > 65535)
+      k_stride < (int64_t)num_kv_heads * head_dim || v_stride < (int64_t)num_kv_heads * head_dim || n_seqs > 65535 ||
+      k_stride > kMaxActStride || v_stride > kMaxActStride)
     return NVAMD_EINVAL;
   PrefillArgs a = {};
   a.out = static_cast<u16 *>(out);
