@@ -98,7 +98,7 @@ __device__ __forceinline__ void load_agent2(const float *p, float &lo, float &hi
 
 // GQA 1, and GQA 2 with one chunk per wave, fit 128 VGPRs without spills: four waves
 // per SIMD.
-template <int GQA, int NW, int CPW, int TILES>
+template <int GQA, int NW, int CPW, int TILES, bool WHOLE>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((GQA == 1 || (GQA == 2 && CPW == 1)) ? 4 : 1)))
 paged_decode_kernel(DecodeArgs a) {
@@ -118,6 +118,14 @@ paged_decode_kernel(DecodeArgs a) {
   const int ctx_cap = min(a.max_ctx, a.bt_width << a.bs_log2);
   const int item = blockIdx.x;
   int b = -1, n_parts = 0, first = 0, ctx = 0;
+  if constexpr (WHOLE) {
+    // One workgroup per (b, g) covers the whole context bound: the item needs no scan, so the
+    // context length, the block-table entries and q are loaded together.
+    b = item / hkv;
+    n_parts = 1;
+    first = b;
+    ctx = max(min(a.context_lens[b], ctx_cap), 0);
+  } else
   for (int b0 = 0, base = 0; b0 < a.batch; b0 += 64) {
     const int bi = b0 + lane;
     int ci = 0, np = 0;
@@ -141,7 +149,7 @@ paged_decode_kernel(DecodeArgs a) {
   if (b < 0) return;  // past the last item
   b = __builtin_amdgcn_readfirstlane(b);
   n_parts = __builtin_amdgcn_readfirstlane(n_parts);
-  ctx = __builtin_amdgcn_readfirstlane(ctx);
+  if constexpr (!WHOLE) ctx = __builtin_amdgcn_readfirstlane(ctx);  // a scalar load already
   const int rem = item - __builtin_amdgcn_readfirstlane(first) * hkv;
   const int g = rem / n_parts;
   const int p = rem - g * n_parts;
@@ -152,6 +160,9 @@ paged_decode_kernel(DecodeArgs a) {
   __shared__ float s_o[NW][2][GQA][D];  // per wave and half-wave: summed row groups
   __shared__ float s_l[NW][2][GQA];
   __shared__ float s_m[NW][GQA];
+
+  const int32_t *bt_row = a.block_tables + (int64_t)b * a.bt_stride;
+  const int t_begin = p * PART + w * WT;
 
   // Query rows of the GQA group, as bf16 pairs for v_dot2.
   u32x4 qr[GQA][2];
@@ -171,12 +182,10 @@ paged_decode_kernel(DecodeArgs a) {
     for (int i = 0; i < 16; ++i) o[j][i] = 0.f;
   }
 
-  const int t_begin = p * PART + w * WT;
   const int t_end = min(t_begin + WT, ctx);
   const int bs_mask = (1 << a.bs_log2) - 1;
   const int64_t row_elems = (int64_t)hkv * D;  // elements between consecutive tokens
   const int64_t step8 = 8 * row_elems;
-  const int32_t *bt_row = a.block_tables + (int64_t)b * a.bt_stride;
 
   if (t_begin < t_end) {
     const int last_tile = (t_end - 1) & ~15;
@@ -439,15 +448,16 @@ paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-template <int GQA, int NW, int CPW, int TILES = 4>
+template <int GQA, int NW, int CPW, int TILES = 4, bool WHOLE = false>
 int launch(DecodeArgs a, int batch, hipStream_t stream) {
   constexpr int PART = NW * CPW * 16 * TILES;
   a.max_parts = ceil_div(a.max_ctx, PART);
   if (a.max_parts > 64) return NVAMD_EUNSUPPORTED;  // merge stage holds <= 64 partitions
+  if (WHOLE && a.max_parts != 1) return NVAMD_EINVAL;
   a.batch = batch;
   // One workgroup per possible (b, g, p); the ones past the last existing item exit at once.
   dim3 grid((unsigned)((int64_t)batch * a.num_kv_heads * a.max_parts));
-  hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW, TILES>), grid, dim3(NW * 64), 0, stream, a);
+  hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW, TILES, WHOLE>), grid, dim3(NW * 64), 0, stream, a);
   return launch_status();
 }
 
@@ -475,11 +485,11 @@ int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
   const int64_t want = 2LL * num_cus();
   if (units * ceil_div(a.max_ctx, 256) < want) {
     const int nw_whole = ceil_div(a.max_ctx, 64);
-    if (nw_whole <= 2) return launch<GQA, 2, 1>(a, batch, stream);
-    if (nw_whole <= 4) return launch<GQA, 4, 1>(a, batch, stream);
-    if (nw_whole <= 8) return launch<GQA, 8, 1>(a, batch, stream);
+    if (nw_whole <= 2) return launch<GQA, 2, 1, 4, true>(a, batch, stream);
+    if (nw_whole <= 4) return launch<GQA, 4, 1, 4, true>(a, batch, stream);
+    if (nw_whole <= 8) return launch<GQA, 8, 1, 4, true>(a, batch, stream);
     if constexpr (GQA <= 2) {  // 16 waves = 4 per SIMD: fits the 128 VGPRs of GQA <= 2
-      if (nw_whole <= 16) return launch<GQA, 16, 1>(a, batch, stream);
+      if (nw_whole <= 16) return launch<GQA, 16, 1, 4, true>(a, batch, stream);
     }
     if (ceil_div(a.max_ctx, 64) <= 64) {
       if (units * ceil_div(a.max_ctx, 128) >= want) return launch<GQA, 2, 1>(a, batch, stream);
