@@ -8,6 +8,7 @@ depends on torch, so the same file serves ctypes, a C harness or any FFI.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -42,12 +43,37 @@ def sources() -> list[Path]:
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
+_REMARK = re.compile(r"remark:\s+(Function Name|ScratchSize \[bytes/lane\]):\s+(\S+)")
+
+
+def scratch_by_kernel(remarks: str) -> dict[str, int]:
+    """Per-kernel scratch bytes per lane from the compiler's kernel-resource-usage remarks."""
+    out: dict[str, int] = {}
+    name = None
+    for key, value in _REMARK.findall(remarks):
+        if key == "Function Name":
+            name = value
+        elif name is not None:
+            out[name] = int(value)
+            name = None
+    return out
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *DEVICE_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
+    # Every kernel here is sized to its register budget; a register spill goes to scratch
+    # memory and silently costs a large factor (one spill in the decode kernel: 1.38x), so
+    # any scratch use fails the build.
+    kernels = scratch_by_kernel(proc.stderr)
+    if not kernels:
+        raise RuntimeError(f"no kernel-resource-usage remarks for {src.name}")
+    spilled = {k: v for k, v in kernels.items() if v}
+    if spilled:
+        raise RuntimeError(f"{src.name}: kernels use scratch (register spills): {spilled}")
     return obj
 
 

@@ -31,3 +31,18 @@ def test_host_only_entry_points():
     big = _C.paged_decode_workspace_size(32, 16, 8, 4096)
     assert 0 < small < big
     assert _C.paged_decode_workspace_size(0, 16, 8, 512) == 0
+
+
+def test_build_rejects_kernels_that_spill_to_scratch():
+    """The build reads the compiler's kernel-resource-usage remarks and fails on any scratch use."""
+    from nano_vllm_ascend_amd.build import scratch_by_kernel
+
+    remarks = "\n".join([
+        "a.hip:10:1: remark: Function Name: _Z3fooPf [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:10:1: remark:     VGPRs: 128 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:10:1: remark:     ScratchSize [bytes/lane]: 116 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:20:1: remark: Function Name: _Z3barPf [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:20:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert scratch_by_kernel(remarks) == {"_Z3fooPf": 116, "_Z3barPf": 0}
+    assert scratch_by_kernel("") == {}
