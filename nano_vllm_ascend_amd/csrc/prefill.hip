@@ -9,12 +9,14 @@
 //          sees keys 0..kv_len-q_len+r (bottom-right causal; prefix-hit route).
 //
 // Workgroup = 4 waves = one kv head g, its GQA query heads, and a tile of
-// BQ = 128/GQA query tokens; wave w owns 32 query rows of one head.  Two
-// workgroups share a CU (two waves per SIMD, 2 x 70 KB of LDS), so one wave's
-// softmax and LDS traffic overlap the other's MFMAs and the two workgroups'
-// per-tile barriers do not hold each other up.
-// Per 64-key tile:
-//   S^T[64 keys x 32 queries] = K . Q^T  with v_mfma_f32_32x32x16_bf16
+// BQ = 128/GQA query tokens; wave w owns 32 query rows of one head.  Three
+// workgroups share a CU (three waves per SIMD at <= 168 VGPRs, 3 x 37 KB of
+// LDS), so one wave's softmax and LDS traffic overlap another's MFMAs and the
+// workgroups' per-tile barriers do not hold each other up.  32-key tiles keep
+// both budgets: 64-key tiles (70 KB, 200 VGPRs) allow two workgroups per CU and
+// measure 1.07x slower.
+// Per 32-key tile:
+//   S^T[32 keys x 32 queries] = K . Q^T  with v_mfma_f32_32x32x16_bf16
 //        (A = K rows from LDS, B = Q rows kept in registers for the whole loop).
 //        In this layout a lane owns ONE query column, so the softmax max/sum
 //        of a query is in-lane plus one exchange with lane^32.
@@ -33,23 +35,23 @@
 // K/V tiles while the XCD's L2 still holds them (a query-tile-major order streams every
 // sequence's K/V from memory once per tile: 1.3x the time).  K/V tiles are
 // double-buffered in LDS: the next tile is loaded into registers while the current
-// one's MFMAs run, then stored into the other slot, so each 64-key tile costs one
-// barrier.
+// one's MFMAs run, then stored into the other slot, so each tile costs one barrier.
 #include "common.h"
 
 namespace nvamd {
 namespace {
 
-constexpr int kBK = 64;            // keys per tile
+constexpr int kBK = 32;            // keys per tile
+constexpr int kBlocks = kBK / 32;  // 32-key MFMA blocks per tile
 constexpr int kKStride = 136;      // LDS row stride (elements) of the K tile: 272 B, spreads banks
-constexpr int kVtStride = 72;      // LDS row stride (elements) of the transposed V tile: 144 B, 16-byte aligned
+constexpr int kVtStride = kBK + 8;  // LDS row stride (elements) of the transposed V tile: 16-byte aligned
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 // Largest K/V activation row stride (elements) of the dense route: a 64-row tile's byte range
 // is a 32-bit buffer size.
 constexpr int64_t kMaxActStride = (int64_t)1 << 24;
 constexpr u32 kBf16PairOne = 0x3F803F80u;  // (1.0, 1.0) as a bf16 pair
 
-// Position of key k of a 64-key tile inside a V^T row.  Within each 16-key group the PV
+// Position of key k of a key tile inside a V^T row.  Within each 16-key group the PV
 // step of lane half h consumes keys {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1); swapping
 // bits 2 and 3 of the key makes each of those sets 8 contiguous elements.
 __device__ __forceinline__ int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
@@ -81,7 +83,7 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8v a, bf16x8v b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-constexpr int kWaves = 4;  // two workgroups per CU (LDS 2 x 70 KB): their barriers are independent
+constexpr int kWaves = 4;  // three workgroups per CU: their barriers are independent
 constexpr int kThreads = kWaves * 64;
 constexpr int kKLoads = kBK * 16 / kThreads;      // 16-byte K chunks per thread per tile
 constexpr int kVLoads = kBK / 2 * 16 / kThreads;  // (key pair, 8-dim chunk) units per thread
@@ -142,7 +144,7 @@ prefill_kernel(PrefillArgs a) {
   // cooperative tile loads: K rows (t>>4) + (threads/16)i, 16-byte chunk t&15; V row pair t&31,
   // 8 dims 8 * ((t>>5) + (threads/32)e)
   const int kr = tid >> 4, kc = tid & 15;
-  const int vp = tid & 31, vc = tid >> 5;
+  const int vp = tid % (kBK / 2), vc = tid / (kBK / 2);
   const int32_t *bt_row = PAGED ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
   const int64_t cache_row = (int64_t)a.num_kv_heads * D;
   const int bs_mask = (1 << a.bs_log2) - 1;
@@ -167,7 +169,7 @@ prefill_kernel(PrefillArgs a) {
     for (int i = 0; i < kVLoads; ++i)
 #pragma unroll
       for (int e = 0; e < 2; ++e)
-        v_off[i][e] = (u32)(((2 * vp + e) * a.v_stride + g * D + 8 * (vc + kThreads / 32 * i)) * 2);
+        v_off[i][e] = (u32)(((2 * vp + e) * a.v_stride + g * D + 8 * (vc + kThreads / (kBK / 2) * i)) * 2);
   }
   auto tile_rsrc = [&](const u16 *act, int64_t stride, int t) {
     const int base = t * kBK;
@@ -194,7 +196,7 @@ prefill_kernel(PrefillArgs a) {
       for (int i = 0; i < kVLoads; ++i)
 #pragma unroll
         for (int e = 0; e < 2; ++e)
-          vreg[i][e] = ld16(row_ptr(a.v_cache, t * kBK + 2 * vp + e) + 8 * (vc + kThreads / 32 * i));
+          vreg[i][e] = ld16(row_ptr(a.v_cache, t * kBK + 2 * vp + e) + 8 * (vc + kThreads / (kBK / 2) * i));
     } else {
       const __amdgpu_buffer_rsrc_t r = tile_rsrc(a.v, a.v_stride, t);
 #pragma unroll
@@ -216,15 +218,15 @@ prefill_kernel(PrefillArgs a) {
     for (int i = 0; i < kVLoads; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int d = 8 * (vc + kThreads / 32 * i) + 2 * e;
+        const int d = 8 * (vc + kThreads / (kBK / 2) * i) + 2 * e;
         *reinterpret_cast<u32 *>(&sVt[slot][d][vpos]) = pair_lo(vreg[i][0][e], vreg[i][1][e]);
         *reinterpret_cast<u32 *>(&sVt[slot][d + 1][vpos]) = pair_hi(vreg[i][0][e], vreg[i][1][e]);
       }
   };
-  // S^T = K Q^T for the 64 keys of a K slot (two 32-key blocks)
-  auto score = [&](int slot, f32x16 (&st)[2]) {
+  // S^T = K Q^T for the keys of a K slot (kBlocks 32-key blocks)
+  auto score = [&](int slot, f32x16 (&st)[kBlocks]) {
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+    for (int blk = 0; blk < kBlocks; ++blk) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) st[blk][i] = 0.f;
 #pragma unroll
@@ -258,7 +260,7 @@ prefill_kernel(PrefillArgs a) {
     }
     const int base = t * kBK;
     if (visible(t)) {
-      f32x16 st[2];
+      f32x16 st[kBlocks];
       score(t & 1, st);
       // mask; key of register i of block blk: base + 32blk + 8(i/4) + 4hl + i%4.  The running
       // max is taken on raw scores (scale > 0) and applied in the exponent's FMA.
@@ -269,14 +271,14 @@ prefill_kernel(PrefillArgs a) {
         // lane's last visible key, relative to the key of register 0 of block 0
         const int lim = min(offset + rq, kv_len - 1) - base - 4 * hl;
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
+        for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
           for (int i = 0; i < 16; ++i)
             if (32 * blk + 8 * (i / 4) + (i % 4) > lim) st[blk][i] = -INFINITY;
       }
       float tmax = -INFINITY;
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
+      for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
         for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[blk][i]);
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.scale_log2e;
@@ -290,9 +292,9 @@ prefill_kernel(PrefillArgs a) {
       }
       const float neg_ref = m_run == -INFINITY ? 0.f : -m_run;
       float psum = 0.f;
-      bf16x8v pf[2][2];
+      bf16x8v pf[kBlocks][2];
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
+      for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           u32x4 packed;
@@ -318,7 +320,7 @@ prefill_kernel(PrefillArgs a) {
       // O^T += V^T P^T; k-slot 8hl+e of step (blk, hh) is key 32blk + 16hh + 8(e/4) + 4hl + e%4,
       // which the permuted V^T layout stores contiguously: one 16-byte read per operand.
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
+      for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const int k0 = 32 * blk + 16 * hh + 8 * hl;

@@ -25,12 +25,15 @@ def make_llm(graph=True, prefix=False, layers=SMALL, num_blocks=96, max_num_seqs
 
 
 # Random N(0, 0.02) weights give logits with std ~0.64 over 151,936 tokens, so the
-# top-2 gap is below 0.02 at a few percent of steps.  bf16 GEMMs that accumulate
-# in a different order than the CPU oracle move logits by ~1e-3..1e-2, so a token
-# may differ exactly there.  The parity bar: per-step logits within LOGIT_TOL of
-# the oracle, and every token that differs is a near-tie (oracle margin < TIE_TOL).
+# top-2 gap is below a few hundredths at a few percent of steps.  bf16 kernels that
+# accumulate in a different order than the CPU oracle move each logit by ~1e-3..3e-2
+# (measured worst per step: 0.031), so a token may differ exactly there: the two
+# logits of a swapped pair can move apart by up to twice that.  The parity bar:
+# per-step logits within LOGIT_TOL of the oracle, every token that differs is a
+# near-tie (oracle margin < TIE_TOL, below twice the measured per-logit error), and
+# at most a tenth of the tokens differ.
 LOGIT_TOL = 0.08
-TIE_TOL = 0.02
+TIE_TOL = 0.05
 
 
 @pytest.mark.gpu
