@@ -201,14 +201,19 @@ paged_decode_kernel(DecodeArgs a) {
         const int64_t off = slot * row_elems + (int64_t)g * D + 8 * c;
         const u16 *kp = a.k_cache + off;
         const u16 *vp = a.v_cache + off;
-        T[i].ka0 = ld16(kp);
-        T[i].ka1 = ld16(kp + 64);
-        T[i].kb0 = ld16(kp + step8);
-        T[i].kb1 = ld16(kp + step8 + 64);
-        T[i].va0 = ld16(vp);
-        T[i].va1 = ld16(vp + 64);
-        T[i].vb0 = ld16(vp + step8);
-        T[i].vb1 = ld16(vp + step8 + 64);
+        // K/V are read once per step.  Bandwidth-bound (split) launches use nontemporal loads,
+        // which keep them from displacing other lines in the L2 (1.08x faster over a
+        // 32 x U[256, 2304] step); latency-bound whole-unit launches use plain loads, whose
+        // round trip is shorter (1.16x faster over a 4 x U[1, 512] step).
+        auto ld = [](const u16 *ptr) { return WHOLE ? ld16(ptr) : ld16_stream(ptr); };
+        T[i].ka0 = ld(kp);
+        T[i].ka1 = ld(kp + 64);
+        T[i].kb0 = ld(kp + step8);
+        T[i].kb1 = ld(kp + step8 + 64);
+        T[i].va0 = ld(vp);
+        T[i].va1 = ld(vp + 64);
+        T[i].vb0 = ld(vp + step8);
+        T[i].vb1 = ld(vp + step8 + 64);
       }
 
       // QK for the chunk: s[tile][row a/b][head]
