@@ -102,7 +102,7 @@ def _paged_case(device, prompt_lens, cached, bs=128, seed=0, hq=16, hkv=8):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("bs", [128, 16])
+@pytest.mark.parametrize("bs", [128, 64, 32, 16])  # >= 32: one descriptor per tile; 16: per-row lookups
 def test_paged_prefix_hit_prefill(device, bs):
     prompt_lens = [300, 129, 1000, 64, 255]
     cached = [256, 128, 384, 0, 128]
