@@ -15,9 +15,12 @@
 // of each 16-row tile, c = lane%8 picks dims 8c..8c+7 and 64+8c..64+8c+7.
 // Eight lanes read one 256-byte K/V row as two whole 128-byte lines.
 //
-// Per 64-token chunk a wave issues all 32 of its 16-byte loads first (32 KB in
-// flight per wave); tiles past the wave's range re-read its last valid tile
-// (a cache hit, not HBM traffic) so the load stream stays branch free.  Then:
+// Per 64-token chunk a wave's 32 16-byte loads (32 KB) come before any math in the
+// source; at 4 waves per SIMD (<= 128 VGPRs) the compiler issues them in register-sized
+// batches behind the per-tile block-table reads, so two or three batches are in flight
+// at a time.  Split launches load K/V nontemporally (read once; no L2 allocation).
+// Tiles past the wave's range re-read its last valid tile (a cache hit, not HBM
+// traffic) so the load stream stays branch free.  Then:
 //   QK:  v_dot2 over bf16 pairs for the whole chunk, 3-step DPP sum over 8 lanes;
 //   softmax: each 8-lane row group keeps its own running max, so a chunk
 //        needs no cross-lane max and no branch -- one rescale per chunk;
@@ -30,8 +33,10 @@
 // NW waves through LDS.  A multi-partition unit's wave 0 then publishes
 // (max, sum, acc[128]) per head with agent-scope write-through stores, waits for
 // them, and bumps an arrival counter; the last to arrive reads the partials with
-// agent-scope loads, all issued before the first is used, and writes the output.  No L2 writeback or
-// invalidate is needed.
+// agent-scope loads, all issued before the first is used, and writes the output.  No L2
+// writeback or invalidate is needed.  Launches with few items (short contexts, small
+// batches) give each (sequence, kv head) one workgroup that covers the whole context
+// bound: no partials and no item scan.
 #include "common.h"
 
 namespace nvamd {

@@ -55,6 +55,16 @@ def test_decode_edge_lengths(device, ctx):
 
 
 @pytest.mark.gpu
+def test_decode_long_contexts_many_partitions(device):
+    """Contexts of 4200-9000 tokens: up to 36 partitions per (sequence, kv head), past the 16 the
+    merge loads in its first round, so later partitions arrive 8 per round."""
+    work = W.make_decode(8, 4200, 9000, 600, seed=17, device=device)
+    assert max(work.context_lens_list) > 16 * 256
+    check(work)
+    check(work, max_ctx=12000)  # a looser bound only adds empty workgroups
+
+
+@pytest.mark.gpu
 def test_decode_large_ragged_batch_with_empty_sequences(device):
     """150 sequences (the work list spans three 64-sequence scans), some with no context."""
     gen = torch.Generator().manual_seed(21)
