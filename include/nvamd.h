@@ -36,7 +36,9 @@ extern "C" {
 #define NVAMD_EUNSUPPORTED (-2) /* head_dim / GQA group / block_size not built */
 #define NVAMD_EWORKSPACE (-3)  /* workspace missing or too small               */
 
-/* Library version, for the loader's sanity check. */
+/* ABI version of this header; nvamd_version() returns the version the library was built
+   with, for the loader's sanity check. */
+#define NVAMD_ABI_VERSION 1
 int nvamd_version(void);
 
 /* ------------------------------------------------------------------------- */

@@ -201,4 +201,4 @@ extern "C" int nvamd_qk_norm_rope(void *q, int64_t q_stride, void *k, int64_t k_
   return launch_status();
 }
 
-extern "C" int nvamd_version(void) { return 1; }
+extern "C" int nvamd_version(void) { return NVAMD_ABI_VERSION; }

@@ -26,7 +26,9 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_host_only_entry_points():
-    assert _C.version() >= 1
+    header = (Path(__file__).resolve().parents[1] / "include" / "nvamd.h").read_text()
+    declared = int(re.search(r"#define NVAMD_ABI_VERSION (\d+)", header).group(1))
+    assert _C.version() == declared
     small = _C.paged_decode_workspace_size(4, 16, 8, 512)
     big = _C.paged_decode_workspace_size(32, 16, 8, 4096)
     assert 0 < small < big
