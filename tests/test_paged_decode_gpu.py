@@ -99,6 +99,20 @@ def test_decode_block_sizes(device, bs):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("heads", [(8, 8), (16, 8), (16, 4)])
+@pytest.mark.parametrize("bs", [16, 128])
+def test_decode_split_path_gqa_and_block_sizes(device, heads, bs):
+    """Batches large enough for the split-KV launch (nontemporal loads, cross-workgroup merge)
+    at every GQA group and a small and a large block size; the small-batch tests above take
+    the whole-unit launch."""
+    hq, hkv = heads
+    work = W.make_decode(48, 300, 900, 48 * 900 // bs + 8, seed=bs + hq, device=device, block_size=bs,
+                         num_heads=hq, num_kv_heads=hkv)
+    assert 48 * hkv * -(-max(work.context_lens_list) // 256) >= 2 * 256  # split launch on a 256-CU GPU
+    check(work)
+
+
+@pytest.mark.gpu
 def test_decode_ignores_stale_rows_past_context(device):
     """Unwritten rows of the last block may hold NaN bit patterns; they must not reach the output."""
     work = W.make_decode(4, 1, 300, 16, seed=3, device=device)
