@@ -166,7 +166,7 @@ skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < kSsqVec; ++i) ss += (sv[mt][i][0] + sv[mt][i][1]) + (sv[mt][i][2] + sv[mt][i][3]);
         ss += swizzle_xor16(ss);
-        ss += __shfl_xor(ss, 32);
+        ss = sum_xor32(ss);
         rstd[mt] = rsqrtf(ss / (float)a.k + a.eps);
       }
     }

@@ -281,7 +281,7 @@ prefill_kernel(PrefillArgs a) {
       for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
         for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[blk][i]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.scale_log2e;
+      tmax = max_xor32(tmax) * a.scale_log2e;
       // Lazy rescale: the exponent's reference moves only when a score exceeds it by more
       // than 2^8, so P <= 256 and O, l are rescaled only on the tiles where some lane's
       // reference moved.  O / l is unchanged by the choice of reference.
@@ -339,7 +339,7 @@ prefill_kernel(PrefillArgs a) {
   }
 
   // normalise and write: register i of block db is dim 32db + 8(i/4) + 4hl + i%4 of query column n
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = sum_xor32(l_run);
   if (!q_ok) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   u16 *op = a.out + q_tok * a.out_stride + (int64_t)head * D + 4 * hl;
