@@ -336,7 +336,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the path shards by sequence or kv head with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the path shards by sequence, or by kv head with one o_proj all-reduce per layer; only the "
+              "one-GPU share is built and measured)", file=sys.stderr)
         sys.exit(2)
 
     import torch
