@@ -11,7 +11,8 @@ them.  Inputs are resident in HBM before the timed region.
 
 Also reported: the roofline of the decode kernel (average launch duration from
 HIP events on the launch stream), the fp32 CPU oracle on the host cores as the
-CPU baseline, the ragged causal prefill of 32 prompts of U[64, 2048] tokens
+CPU baseline, the same decode step with the per-head q/k norm, RoPE and KV store fused into
+the attention launch (against the two-launch chain), the ragged causal prefill of 32 prompts of U[64, 2048] tokens
 (TFLOP/s against the dense bf16 MFMA peak) with its paged KV store (GB/s), and
 (unless --no-e2e) the end-to-end output tok/s of the 32 x 256-in / 2048-out
 greedy workload next to the reference's published 910B3 figure.
@@ -137,6 +138,65 @@ def decode_leg(args, device):
     }
 
 
+def fused_step_leg(args, work, device) -> dict:
+    """The decode step of the same 32 sequences as a model layer runs it: per-head q/k RMSNorm
+    (eps 1e-6, weights N(1, 0.02)), RoPE (theta 1e6), the KV store of the new tokens through
+    slot_mapping, then paged attention -- as two launches (qk_norm_rope with the store, then
+    paged_decode) and as the one fused launch (nvamd_paged_decode_fused), over the 28 layers'
+    pools.  HIP events around `steps` eager passes; microseconds per layer."""
+    import torch
+
+    from nano_vllm_ascend_amd import _C
+    from nano_vllm_ascend_amd import workloads as W
+    from nano_vllm_ascend_amd.layers import RotaryEmbedding
+
+    inp = W.fused_step_inputs(work, args.seed, device)
+    table = RotaryEmbedding(W.HEAD_DIM, 40960, W.ROPE_THETA).cos_sin.to(device)
+    b = inp.qkv.shape[0]
+    hq, hkv, d = W.NUM_HEADS, W.NUM_KV_HEADS, W.HEAD_DIM
+    max_ctx = max(work.context_lens_list)
+    scale = d ** -0.5
+    ws = _C.alloc_paged_decode_workspace(b, hq, hkv, max_ctx, device)
+    out = torch.empty(b, hq, d, dtype=torch.bfloat16, device=device)
+    raw = inp.qkv
+    def views(qkv):
+        return (qkv[:, : hq * d].view(b, hq, d), qkv[:, hq * d : (hq + hkv) * d].view(b, hkv, d),
+                qkv[:, (hq + hkv) * d :].view(b, hkv, d))
+
+    q, k, v = views(raw)
+    q2, k2, v2 = views(raw.clone())  # the two-launch chain rewrites q and k in place
+    layers = [(work.key_cache[l], work.value_cache[l]) for l in range(NUM_LAYERS)]
+
+    def two_launches():
+        for kc, vc in layers:
+            _C.qk_norm_rope(q2, k2, inp.q_weight, inp.k_weight, inp.positions, table, W.RMS_EPS, v=v2, key_cache=kc,
+                            value_cache=vc, slot_mapping=inp.slot_mapping)
+            _C.paged_decode(out, q2, kc, vc, work.block_tables, work.context_lens, scale, max_ctx, ws)
+
+    def fused():
+        for kc, vc in layers:
+            _C.paged_decode_fused(out, q, k, v, inp.q_weight, inp.k_weight, inp.positions, table, W.RMS_EPS, kc, vc,
+                                  inp.slot_mapping, work.block_tables, work.context_lens, scale, max_ctx, ws)
+
+    def us_per_layer(fn, reps=20):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * NUM_LAYERS)
+
+    two = us_per_layer(two_launches)
+    one = us_per_layer(fused)
+    return {"workload": "decode step, 32 seqs, context U[256, 2304]: q/k norm + RoPE + KV store + attention",
+            "two_launches_us_per_layer": round(two, 3), "fused_us_per_layer": round(one, 3),
+            "saved_us_per_layer": round(two - one, 3)}
+
+
 def small_decode_leg(args, device) -> dict:
     """Single-layer decode shape of 4 sequences, context U[1, 512], 64-block pools: as 28 launches
     (one per layer, each its own pool, 0.9 GB in total) captured in one hipGraph, and as one eager
@@ -241,7 +301,8 @@ def prefill_leg(args, device) -> dict:
                       "tflops": round(tflops, 1), "bound": "mfma", "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
                       "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
         "kv_store": {"kernel": "kv_cache_write_kernel", "us": round(us_store, 2), "bytes": store_bytes,
-                     "gbs": round(store_bytes / us_store / 1e3, 1), "frac": round(store_bytes / us_store / 1e3 / HBM_PEAK_GBS, 4)},
+                     "gbs": round(store_bytes / us_store / 1e3, 1),
+                     "frac": round(store_bytes / us_store / 1e3 / HBM_PEAK_GBS, 4)},
     }
 
 
@@ -392,6 +453,7 @@ def main():
             "median_launch_us": round(dec["median_launch_us"], 3),
         },
     }
+    result["fused_step"] = fused_step_leg(args, dec["work"], device)
     small = small_decode_leg(args, device)
     result["decode_small"] = {k: v for k, v in small.items() if k != "work"}
     if not args.no_cpu:

@@ -74,7 +74,38 @@ int nvamd_paged_decode(void *out, int64_t out_stride,
                        hipStream_t stream);
 
 /* ------------------------------------------------------------------------- */
-/* P2: paged KV store.                                                        */
+/* P5 + P2 + P4 fused: one decode step of a layer's attention.                */
+/* Replaces the sequence Qwen3Attention.forward runs for a decode batch       */
+/* (nv/models/qwen3.py:83-96 then :105-112): q_norm/k_norm, RoPE, kv write    */
+/* of post-RoPE k and raw v at slot_mapping, then paged attention.            */
+/* Equivalent to nvamd_qk_norm_rope(q, k, v, ..., k_cache, v_cache,          */
+/* slot_mapping) followed by nvamd_paged_decode over the normalised q, bit    */
+/* for bit, provided slot_mapping[i] is the cache slot of row positions[i]   */
+/* of sequence i's block table (as the block manager builds decode metadata:  */
+/* position = context_lens[i] - 1).  q, k, v are the raw projection rows      */
+/* [batch, *] and are NOT rewritten (only out and the cache are written).     */
+/* q_weight, k_weight, cos_sin and every row stride: 16-byte aligned.         */
+/* Workspace rules as for nvamd_paged_decode.                                 */
+/* ------------------------------------------------------------------------- */
+int nvamd_paged_decode_fused(void *out, int64_t out_stride,
+                             const void *q, int64_t q_stride,
+                             const void *k, int64_t k_stride,
+                             const void *v, int64_t v_stride,
+                             const void *q_weight, const void *k_weight,
+                             const int64_t *positions,
+                             const float *cos_sin, int max_positions, float eps,
+                             void *k_cache, void *v_cache,
+                             int num_blocks, int block_size,
+                             const int64_t *slot_mapping,
+                             const int32_t *block_tables, int bt_stride, int bt_width,
+                             const int32_t *context_lens,
+                             int batch, int num_heads, int num_kv_heads, int head_dim,
+                             float scale, int max_context_len,
+                             void *workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* P2: paged KV store.                                                       */
 /* Replaces PagedKVCache.write (nv/npu/paged_kv_cache.py:44-69): the two      */
 /* index_copy_ calls  cache_flat[slot_mapping[t]] = kv[t]  for K and V.       */
 /* A negative slot skips that token (padding rows).                           */

@@ -34,6 +34,12 @@ _SIGNATURES = {
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_ptr,
          _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_ptr, _c_size, _c_ptr],
     ),
+    "nvamd_paged_decode_fused": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,
+         _c_float, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_int,
+         _c_int, _c_float, _c_int, _c_ptr, _c_size, _c_ptr],
+    ),
     "nvamd_kv_cache_write": (
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_i64, _c_ptr],
@@ -180,6 +186,54 @@ def paged_decode(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, va
         workspace.numel() * workspace.element_size(), _stream(),
     )
     _check(status, "nvamd_paged_decode")
+    return out
+
+
+def paged_decode_fused(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       q_weight: torch.Tensor, k_weight: torch.Tensor, positions: torch.Tensor,
+                       cos_sin: torch.Tensor, eps: float, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                       slot_mapping: torch.Tensor, block_tables: torch.Tensor, context_lens: torch.Tensor,
+                       scale: float, max_context_len: int, workspace: torch.Tensor) -> torch.Tensor:
+    """One decode step of attention: qk_norm_rope (with the KV store) then paged_decode, in one launch.
+
+    q: raw [B, Hq, 128] and k, v: raw [B, Hkv, 128] rows of the new tokens (views into the
+    projection output are fine; they are not modified).  Writes out and the caches only.
+    slot_mapping[i] must be the cache slot of row positions[i] of sequence i (decode metadata).
+    """
+    lib = load()
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("key_cache", key_cache),
+                    ("value_cache", value_cache)):
+        _bf16_cuda(name, t)
+    _require(q.dim() == 3 and out.shape == q.shape, f"q/out shape mismatch: {tuple(q.shape)} vs {tuple(out.shape)}")
+    _require(k.dim() == 3 and k.shape == v.shape and k.shape[0] == q.shape[0], "k/v must be [B, Hkv, D]")
+    _require(key_cache.dim() == 4 and key_cache.shape == value_cache.shape, "key/value cache shape mismatch")
+    _require(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    nb, bs, hkv, d = key_cache.shape
+    b, hq, dq = q.shape
+    _require(dq == d and k.shape[1:] == (hkv, d), f"head shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}")
+    _require(q_weight.dtype == torch.bfloat16 and k_weight.dtype == torch.bfloat16, "norm weights must be bf16")
+    _require(q_weight.numel() == d and k_weight.numel() == d, "norm weights must have head_dim elements")
+    _require(q_weight.is_contiguous() and k_weight.is_contiguous(), "norm weights must be contiguous")
+    _require(positions.dtype == torch.int64 and positions.numel() == b and positions.is_cuda,
+             "positions must be int64 [B] on the device")
+    _require(cos_sin.dtype == torch.float32 and cos_sin.dim() == 2 and cos_sin.shape[1] == d and cos_sin.is_cuda
+             and cos_sin.is_contiguous(), "cos_sin must be contiguous fp32 [max_positions, head_dim]")
+    _require(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == b and slot_mapping.is_cuda,
+             "slot_mapping must be int64 [B] on the device")
+    _require(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and block_tables.shape[0] == b,
+             "block_tables must be int32 [B, W]")
+    _require(block_tables.stride(1) == 1, "block_tables rows must be dense")
+    _require(context_lens.dtype == torch.int32 and context_lens.numel() == b and context_lens.is_cuda
+             and context_lens.is_contiguous(), "context_lens must be int32 [B] on the device")
+    status = lib.nvamd_paged_decode_fused(
+        out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), k.data_ptr(), _row_stride(k),
+        v.data_ptr(), _row_stride(v), q_weight.data_ptr(), k_weight.data_ptr(), positions.contiguous().data_ptr(),
+        cos_sin.data_ptr(), cos_sin.shape[0], float(eps), key_cache.data_ptr(), value_cache.data_ptr(), nb, bs,
+        slot_mapping.contiguous().data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
+        block_tables.shape[1], context_lens.data_ptr(), b, hq, hkv, d, float(scale), int(max_context_len),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(),
+    )
+    _check(status, "nvamd_paged_decode_fused")
     return out
 
 

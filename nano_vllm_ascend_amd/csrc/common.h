@@ -44,6 +44,20 @@ __device__ __forceinline__ u16 f32_to_bf16(float x) {
 }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+// Per-head RMSNorm + rotate-half RoPE, element steps shared by every kernel that applies them,
+// so each rounds identically: fp32 arithmetic, the normalised value rounded to bf16 before the
+// rotation (nv/layers/layernorm.py:12-17, nv/layers/rotary_embedding.py:20-42).
+// Sum of squares of the dims (d, d+1, 64+d, 65+d); the 32 such partials of a head are summed
+// as a balanced tree in order of d.
+__device__ __forceinline__ float head_ssq4(float x0, float x1, float x2, float x3) {
+  return x0 * x0 + x1 * x1 + x2 * x2 + x3 * x3;
+}
+__device__ __forceinline__ float head_rstd(float ss, float eps) { return rsqrtf(ss * (1.0f / kHeadDim) + eps); }
+__device__ __forceinline__ float head_norm(float x, float rstd, float w) { return round_bf16(x * rstd * w); }
+// out[d] = y[d] cos[d] - y[d+64] sin[d];  out[d+64] = y[d+64] cos[d] + y[d] sin[d]  (d < 64)
+__device__ __forceinline__ float rope_lo(float y_lo, float y_hi, float c, float s) { return y_lo * c - y_hi * s; }
+__device__ __forceinline__ float rope_hi(float y_lo, float y_hi, float c, float s) { return y_hi * c + y_lo * s; }
+
 // acc + a.lo*b.lo + a.hi*b.hi with bf16 pairs and fp32 accumulation.
 __device__ __forceinline__ float dot2_bf16(u32 a, u32 b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a),

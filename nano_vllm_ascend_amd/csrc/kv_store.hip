@@ -101,16 +101,16 @@ qk_norm_rope_kernel(NormRopeArgs a) {
   const u32 w_hi = *reinterpret_cast<const u32 *>(wt + 64 + d0);
   const float x0 = bf16_lo(x_lo), x1 = bf16_hi(x_lo), x2 = bf16_lo(x_hi), x3 = bf16_hi(x_hi);
 
-  float ss = x0 * x0 + x1 * x1 + x2 * x2 + x3 * x3;
+  float ss = head_ssq4(x0, x1, x2, x3);
   ss = sum16(ss);
-  ss += swizzle_xor16(ss);  // the 32 lanes of this half-wave
-  const float rstd = rsqrtf(ss * (1.0f / kHeadDim) + a.eps);
+  ss += swizzle_xor16(ss);  // the 32 lanes of this half-wave: a balanced tree in lane order
+  const float rstd = head_rstd(ss, a.eps);
 
   // RMSNorm output rounded to bf16 (the reference's norm returns bf16).
-  const float y0 = round_bf16(x0 * rstd * bf16_lo(w_lo));
-  const float y1 = round_bf16(x1 * rstd * bf16_hi(w_lo));
-  const float y2 = round_bf16(x2 * rstd * bf16_lo(w_hi));
-  const float y3 = round_bf16(x3 * rstd * bf16_hi(w_hi));
+  const float y0 = head_norm(x0, rstd, bf16_lo(w_lo));
+  const float y1 = head_norm(x1, rstd, bf16_hi(w_lo));
+  const float y2 = head_norm(x2, rstd, bf16_lo(w_hi));
+  const float y3 = head_norm(x3, rstd, bf16_hi(w_hi));
 
   int64_t pos = a.positions[t];
   pos = pos < 0 ? 0 : (pos >= a.max_positions ? a.max_positions - 1 : pos);
@@ -118,9 +118,8 @@ qk_norm_rope_kernel(NormRopeArgs a) {
   const float c0 = round_bf16(cs[d0]), c1 = round_bf16(cs[d0 + 1]);
   const float s0 = round_bf16(cs[64 + d0]), s1 = round_bf16(cs[64 + d0 + 1]);
 
-  // out[d] = y[d] cos[d] - y[d+64] sin[d];  out[d+64] = y[d+64] cos[d] + y[d] sin[d]
-  const u32 o_lo = pack_bf16x2(y0 * c0 - y2 * s0, y1 * c1 - y3 * s1);
-  const u32 o_hi = pack_bf16x2(y2 * c0 + y0 * s0, y3 * c1 + y1 * s1);
+  const u32 o_lo = pack_bf16x2(rope_lo(y0, y2, c0, s0), rope_lo(y1, y3, c1, s1));
+  const u32 o_hi = pack_bf16x2(rope_hi(y0, y2, c0, s0), rope_hi(y1, y3, c1, s1));
   *reinterpret_cast<u32 *>(x + d0) = o_lo;
   *reinterpret_cast<u32 *>(x + 64 + d0) = o_hi;
   if (!is_q && slot >= 0) {

@@ -37,6 +37,13 @@
 // writeback or invalidate is needed.  Launches with few items (short contexts, small
 // batches) give each (sequence, kv head) one workgroup that covers the whole context
 // bound: no partials and no item scan.
+//
+// Fused decode step (nvamd_paged_decode_fused): the same kernel also runs the per-head
+// RMSNorm + RoPE of the raw query rows (each wave normalises its GQA rows while its first
+// K/V loads are in flight) and of the new token's k, and stores that k and the raw v at
+// slots[b] -- one launch instead of qk_norm_rope + decode, with identical results: the
+// norm's partial sums are combined in the same balanced tree as the standalone kernel's.
+// The wave whose chunk holds the new token's row stores it before loading its chunk.
 #include "common.h"
 
 namespace nvamd {
@@ -70,6 +77,20 @@ struct DecodeArgs {
   int max_ctx;
   int batch;
   float scale_log2e;
+  // Fused decode step only: q holds the raw projection rows; the kernel applies the per-head
+  // RMSNorm and RoPE to q and to the new token's k, and stores that k and the raw v at slots[b].
+  const u16 *k_new;
+  int64_t k_new_stride;
+  const u16 *v_new;
+  int64_t v_new_stride;
+  const u16 *q_w;
+  const u16 *k_w;
+  const int64_t *positions;
+  const float *cos_sin;
+  const int64_t *slots;
+  int64_t num_slots;
+  int max_positions;
+  float eps;
 };
 
 struct KVTile {
@@ -77,6 +98,29 @@ struct KVTile {
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Per-head RMSNorm + RoPE of one head vector held in this kernel's lane layout: the 8 lanes of a
+// row group hold dims 8c..8c+7 (lo) and 64+8c..64+8c+7 (hi).  cs/sn are the bf16-rounded cos/sin
+// of dims 8c..8c+7.  A lane forms the partial sums of squares of the dim quads (d, d+1, 64+d,
+// 65+d) it holds, pairs them, and the 8-lane reduction finishes the same balanced tree over the
+// 32 quads that the standalone norm kernel computes, so both give identical bits.
+__device__ __forceinline__ void head_norm_rope(u32x4 &lo, u32x4 &hi, const u32x4 w_lo, const u32x4 w_hi,
+                                               const float (&cs)[8], const float (&sn)[8], float eps) {
+  float p[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) p[e] = head_ssq4(bf16_lo(lo[e]), bf16_hi(lo[e]), bf16_lo(hi[e]), bf16_hi(hi[e]));
+  const float rstd = head_rstd(sum8((p[0] + p[1]) + (p[2] + p[3])), eps);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float y0 = head_norm(bf16_lo(lo[e]), rstd, bf16_lo(w_lo[e]));
+    const float y1 = head_norm(bf16_hi(lo[e]), rstd, bf16_hi(w_lo[e]));
+    const float y2 = head_norm(bf16_lo(hi[e]), rstd, bf16_lo(w_hi[e]));
+    const float y3 = head_norm(bf16_hi(hi[e]), rstd, bf16_hi(w_hi[e]));
+    const float c0 = cs[2 * e], c1 = cs[2 * e + 1], s0 = sn[2 * e], s1 = sn[2 * e + 1];
+    lo[e] = pack_bf16x2(rope_lo(y0, y2, c0, s0), rope_lo(y1, y3, c1, s1));
+    hi[e] = pack_bf16x2(rope_hi(y0, y2, c0, s0), rope_hi(y1, y3, c1, s1));
+  }
+}
 
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
@@ -103,7 +147,7 @@ __device__ __forceinline__ void load_agent2(const float *p, float &lo, float &hi
 
 // GQA 1, and GQA 2 with one chunk per wave, fit 128 VGPRs without spills: four waves
 // per SIMD.
-template <int GQA, int NW, int CPW, int TILES, bool WHOLE>
+template <int GQA, int NW, int CPW, int TILES, bool WHOLE, bool FUSED>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((GQA == 1 || (GQA == 2 && CPW == 1)) ? 4 : 1)))
 paged_decode_kernel(DecodeArgs a) {
@@ -123,6 +167,7 @@ paged_decode_kernel(DecodeArgs a) {
   const int ctx_cap = min(a.max_ctx, a.bt_width << a.bs_log2);
   const int item = blockIdx.x;
   int b = -1, n_parts = 0, first = 0, ctx = 0;
+  int64_t nr = -1;  // fused step: the new token's position (its row in the context)
   if constexpr (WHOLE) {
     // One workgroup per (b, g) covers the whole context bound: the item needs no scan, so the
     // context length, the block-table entries and q are loaded together.
@@ -130,13 +175,16 @@ paged_decode_kernel(DecodeArgs a) {
     n_parts = 1;
     first = b;
     ctx = max(min(a.context_lens[b], ctx_cap), 0);
+    if constexpr (FUSED) nr = a.positions[b];
   } else
   for (int b0 = 0, base = 0; b0 < a.batch; b0 += 64) {
     const int bi = b0 + lane;
     int ci = 0, np = 0;
+    int64_t pi = 0;
     if (bi < a.batch) {
       ci = max(min(a.context_lens[bi], ctx_cap), 0);
       np = max(ceil_div(ci, PART), 1);
+      if constexpr (FUSED) pi = a.positions[bi];  // with the lengths: no later round trip
     }
     const int incl = wave_incl_scan(np, lane);
     const int total = __shfl(incl, 63);
@@ -147,6 +195,10 @@ paged_decode_kernel(DecodeArgs a) {
       n_parts = __shfl(np, sel);
       first = base + __shfl(incl, sel) - n_parts;
       ctx = __shfl(ci, sel);
+      if constexpr (FUSED) {
+        const int lo = __shfl((int)(uint32_t)pi, sel), hi = __shfl((int)(pi >> 32), sel);
+        nr = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+      }
       break;
     }
     base += total;
@@ -154,7 +206,14 @@ paged_decode_kernel(DecodeArgs a) {
   if (b < 0) return;  // past the last item
   b = __builtin_amdgcn_readfirstlane(b);
   n_parts = __builtin_amdgcn_readfirstlane(n_parts);
-  if constexpr (!WHOLE) ctx = __builtin_amdgcn_readfirstlane(ctx);  // a scalar load already
+  if constexpr (!WHOLE) {
+    ctx = __builtin_amdgcn_readfirstlane(ctx);  // a scalar load already
+    if constexpr (FUSED) {
+      const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)nr);
+      const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)nr >> 32));
+      nr = (int64_t)(((uint64_t)hi << 32) | lo);
+    }
+  }
   const int rem = item - __builtin_amdgcn_readfirstlane(first) * hkv;
   const int g = rem / n_parts;
   const int p = rem - g * n_parts;
@@ -192,6 +251,79 @@ paged_decode_kernel(DecodeArgs a) {
   const int64_t row_elems = (int64_t)hkv * D;  // elements between consecutive tokens
   const int64_t step8 = 8 * row_elems;
 
+  // Fused step: the wave that will read the new token's row (its position nr, when it lies
+  // inside the attended context; else wave 0 of the unit's last item) first stores the token's
+  // post-RoPE k and raw v at slots[b] and waits for the stores to be acknowledged, so its own
+  // K/V loads below read those values back (a wave's loads issued after its acknowledged stores
+  // see them).  No other wave reads that row.  The rope row and norm weights are loaded before
+  // the chunk's K/V loads and the query rows are normalised after those are issued, in the
+  // same branch-free block, so the normalisation overlaps the K/V round trip.
+  f32x4 rc0 = {}, rc1 = {}, rs0 = {}, rs1 = {};
+  u32x4 qw0 = {}, qw1 = {};
+  // The first chunk's block-table entries are read before the owner's store: after a store the
+  // compiler cannot prove the table unchanged and would read it with vector loads, which then
+  // queue behind the rope and K/V loads instead of completing on the scalar path.
+  int first_blk[TILES] = {};
+  if constexpr (FUSED) {
+    if (t_begin < t_end) {
+      const int last = (min(t_begin + WT, ctx) - 1) & ~15;
+#pragma unroll
+      for (int i = 0; i < TILES; ++i) first_blk[i] = bt_row[min(t_begin + 16 * i, last) >> a.bs_log2];
+    }
+  }
+  auto rope_row = [&](float (&cs)[8], float (&sn)[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      cs[e] = round_bf16(rc0[e]);
+      cs[4 + e] = round_bf16(rc1[e]);
+      sn[e] = round_bf16(rs0[e]);
+      sn[4 + e] = round_bf16(rs1[e]);
+    }
+  };
+  auto norm_queries = [&]() {
+    float cs[8], sn[8];
+    rope_row(cs, sn);
+#pragma unroll
+    for (int j = 0; j < GQA; ++j) head_norm_rope(qr[j][0], qr[j][1], qw0, qw1, cs, sn, a.eps);
+  };
+  if constexpr (FUSED) {
+    const bool nr_in = nr >= 0 && nr < ctx;
+    const bool owner = nr_in ? (nr >= t_begin && nr < t_end) : (p == n_parts - 1 && w == 0);
+    if (t_begin < t_end || owner) {
+      const int64_t pc = nr < 0 ? 0 : (nr >= a.max_positions ? a.max_positions - 1 : nr);
+      const float *row = a.cos_sin + pc * D + 8 * c;
+      rc0 = *reinterpret_cast<const f32x4 *>(row);
+      rc1 = *reinterpret_cast<const f32x4 *>(row + 4);
+      rs0 = *reinterpret_cast<const f32x4 *>(row + 64);
+      rs1 = *reinterpret_cast<const f32x4 *>(row + 68);
+      qw0 = ld16(a.q_w + 8 * c);
+      qw1 = ld16(a.q_w + 64 + 8 * c);
+    }
+    if (owner) {
+      const u16 *kp = a.k_new + (int64_t)b * a.k_new_stride + g * D + 8 * c;
+      const u16 *vp = a.v_new + (int64_t)b * a.v_new_stride + g * D + 8 * c;
+      u32x4 k0 = ld16(kp), k1 = ld16(kp + 64);
+      const u32x4 v0 = ld16(vp), v1 = ld16(vp + 64);
+      float cs[8], sn[8];
+      rope_row(cs, sn);
+      head_norm_rope(k0, k1, ld16(a.k_w + 8 * c), ld16(a.k_w + 64 + 8 * c), cs, sn, a.eps);
+      const int64_t slot = a.slots[b];
+      if (r == 0 && slot >= 0 && slot < a.num_slots) {
+        const int64_t dst = slot * row_elems + (int64_t)g * D + 8 * c;
+        u16 *kc = const_cast<u16 *>(a.k_cache);
+        u16 *vc = const_cast<u16 *>(a.v_cache);
+        st16(kc + dst, k0);
+        st16(kc + dst + 64, k1);
+        st16(vc + dst, v0);
+        st16(vc + dst + 64, v1);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // vmcnt counts stores on gfx9: they are acknowledged
+    }
+    if constexpr (CPW > 1) {  // several chunks per wave: normalise once, before the loop
+      if (t_begin < t_end) norm_queries();
+    }
+  }
+
   if (t_begin < t_end) {
     const int last_tile = (t_end - 1) & ~15;
 #pragma unroll 1
@@ -200,7 +332,7 @@ paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < TILES; ++i) {
         const int t0 = min(tc + 16 * i, last_tile);
-        int blk = bt_row[t0 >> a.bs_log2];
+        int blk = (FUSED && CPW == 1) ? first_blk[i] : bt_row[t0 >> a.bs_log2];
         blk = min(max(blk, 0), a.num_blocks - 1);  // never leave the pool
         const int64_t slot = ((int64_t)blk << a.bs_log2) + (t0 & bs_mask) + r;
         const int64_t off = slot * row_elems + (int64_t)g * D + 8 * c;
@@ -220,7 +352,7 @@ paged_decode_kernel(DecodeArgs a) {
         T[i].vb0 = ld(vp + step8);
         T[i].vb1 = ld(vp + step8 + 64);
       }
-
+      if constexpr (FUSED && CPW == 1) norm_queries();  // the wave's only chunk
       // QK for the chunk: s[tile][row a/b][head]
       float s[TILES][2][GQA];
 #pragma unroll
@@ -458,7 +590,7 @@ paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-template <int GQA, int NW, int CPW, int TILES = 4, bool WHOLE = false>
+template <int GQA, int NW, int CPW, int TILES = 4, bool WHOLE = false, bool FUSED = false>
 int launch(DecodeArgs a, int batch, hipStream_t stream) {
   constexpr int PART = NW * CPW * 16 * TILES;
   a.max_parts = ceil_div(a.max_ctx, PART);
@@ -467,7 +599,7 @@ int launch(DecodeArgs a, int batch, hipStream_t stream) {
   a.batch = batch;
   // One workgroup per possible (b, g, p); the ones past the last existing item exit at once.
   dim3 grid((unsigned)((int64_t)batch * a.num_kv_heads * a.max_parts));
-  hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW, TILES, WHOLE>), grid, dim3(NW * 64), 0, stream, a);
+  hipLaunchKernelGGL((paged_decode_kernel<GQA, NW, CPW, TILES, WHOLE, FUSED>), grid, dim3(NW * 64), 0, stream, a);
   return launch_status();
 }
 
@@ -484,7 +616,7 @@ int num_cus() {
   return cus;
 }
 
-template <int GQA>
+template <int GQA, bool FUSED>
 int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
   // 256-token partitions of 4 waves (measured best on MI355X for 32 x ~1.3k contexts).  A launch
   // whose context bound gives fewer than two such items per CU is latency-bound: with a bound of
@@ -495,24 +627,24 @@ int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
   const int64_t want = 2LL * num_cus();
   if (units * ceil_div(a.max_ctx, 256) < want) {
     const int nw_whole = ceil_div(a.max_ctx, 64);
-    if (nw_whole <= 2) return launch<GQA, 2, 1, 4, true>(a, batch, stream);
-    if (nw_whole <= 4) return launch<GQA, 4, 1, 4, true>(a, batch, stream);
-    if (nw_whole <= 8) return launch<GQA, 8, 1, 4, true>(a, batch, stream);
+    if (nw_whole <= 2) return launch<GQA, 2, 1, 4, true, FUSED>(a, batch, stream);
+    if (nw_whole <= 4) return launch<GQA, 4, 1, 4, true, FUSED>(a, batch, stream);
+    if (nw_whole <= 8) return launch<GQA, 8, 1, 4, true, FUSED>(a, batch, stream);
     if constexpr (GQA <= 2) {  // 16 waves = 4 per SIMD: fits the 128 VGPRs of GQA <= 2
-      if (nw_whole <= 16) return launch<GQA, 16, 1, 4, true>(a, batch, stream);
+      if (nw_whole <= 16) return launch<GQA, 16, 1, 4, true, FUSED>(a, batch, stream);
     }
     if (ceil_div(a.max_ctx, 64) <= 64) {
-      if (units * ceil_div(a.max_ctx, 128) >= want) return launch<GQA, 2, 1>(a, batch, stream);
-      return launch<GQA, 1, 1>(a, batch, stream);
+      if (units * ceil_div(a.max_ctx, 128) >= want) return launch<GQA, 2, 1, 4, false, FUSED>(a, batch, stream);
+      return launch<GQA, 1, 1, 4, false, FUSED>(a, batch, stream);
     }
   }
   int cpw = 1;
   while (ceil_div(a.max_ctx, 256 * cpw) > 64) cpw *= 2;
   switch (cpw) {
-    case 1: return launch<GQA, 4, 1>(a, batch, stream);
-    case 2: return launch<GQA, 4, 2>(a, batch, stream);
-    case 4: return launch<GQA, 4, 4>(a, batch, stream);
-    case 8: return launch<GQA, 4, 8>(a, batch, stream);
+    case 1: return launch<GQA, 4, 1, 4, false, FUSED>(a, batch, stream);
+    case 2: return launch<GQA, 4, 2, 4, false, FUSED>(a, batch, stream);
+    case 4: return launch<GQA, 4, 4, 4, false, FUSED>(a, batch, stream);
+    case 8: return launch<GQA, 4, 8, 4, false, FUSED>(a, batch, stream);
     default: return NVAMD_EUNSUPPORTED;
   }
 }
@@ -531,13 +663,14 @@ extern "C" size_t nvamd_paged_decode_workspace_size(int max_batch, int num_heads
   return kCounterBytes + units * parts * gqa * kPartFloats * sizeof(float);
 }
 
-extern "C" int nvamd_paged_decode(void *out, int64_t out_stride, const void *q, int64_t q_stride,
-                                  const void *k_cache, const void *v_cache, int num_blocks, int block_size,
-                                  const int32_t *block_tables, int bt_stride, int bt_width,
-                                  const int32_t *context_lens, int batch, int num_heads, int num_kv_heads,
-                                  int head_dim, float scale, int max_context_len, void *workspace,
-                                  size_t workspace_bytes, hipStream_t stream) {
-  if (batch == 0) return NVAMD_OK;
+namespace {
+
+// Argument checks and DecodeArgs shared by the plain and the fused entry points.
+int fill_decode_args(DecodeArgs &a, void *out, int64_t out_stride, const void *q, int64_t q_stride,
+                     const void *k_cache, const void *v_cache, int num_blocks, int block_size,
+                     const int32_t *block_tables, int bt_stride, int bt_width, const int32_t *context_lens, int batch,
+                     int num_heads, int num_kv_heads, int head_dim, float scale, int max_context_len, void *workspace,
+                     size_t workspace_bytes) {
   if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens) return NVAMD_EINVAL;
   if (batch < 0 || num_blocks <= 0 || num_kv_heads <= 0 || num_heads <= 0 || bt_width <= 0 ||
       bt_stride < bt_width || max_context_len <= 0)
@@ -554,7 +687,7 @@ extern "C" int nvamd_paged_decode(void *out, int64_t out_stride, const void *q, 
   if (!workspace || workspace_bytes < need) return NVAMD_EWORKSPACE;
   if (!aligned16(workspace)) return NVAMD_EINVAL;
 
-  DecodeArgs a;
+  a = DecodeArgs{};
   a.out = static_cast<u16 *>(out);
   a.out_stride = out_stride;
   a.q = static_cast<const u16 *>(q);
@@ -573,11 +706,68 @@ extern "C" int nvamd_paged_decode(void *out, int64_t out_stride, const void *q, 
   a.max_ctx = max_context_len;
   a.max_parts = 0;
   a.scale_log2e = scale * kLog2e;
+  return NVAMD_OK;
+}
 
-  switch (num_heads / num_kv_heads) {
-    case 1: return dispatch<1>(a, batch, stream);
-    case 2: return dispatch<2>(a, batch, stream);
-    case 4: return dispatch<4>(a, batch, stream);
+template <bool FUSED>
+int dispatch_gqa(const DecodeArgs &a, int gqa, int batch, hipStream_t stream) {
+  switch (gqa) {
+    case 1: return dispatch<1, FUSED>(a, batch, stream);
+    case 2: return dispatch<2, FUSED>(a, batch, stream);
+    case 4: return dispatch<4, FUSED>(a, batch, stream);
     default: return NVAMD_EUNSUPPORTED;
   }
+}
+
+}  // namespace
+
+extern "C" int nvamd_paged_decode(void *out, int64_t out_stride, const void *q, int64_t q_stride,
+                                  const void *k_cache, const void *v_cache, int num_blocks, int block_size,
+                                  const int32_t *block_tables, int bt_stride, int bt_width,
+                                  const int32_t *context_lens, int batch, int num_heads, int num_kv_heads,
+                                  int head_dim, float scale, int max_context_len, void *workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+  if (batch == 0) return NVAMD_OK;
+  DecodeArgs a;
+  const int st = fill_decode_args(a, out, out_stride, q, q_stride, k_cache, v_cache, num_blocks, block_size,
+                                  block_tables, bt_stride, bt_width, context_lens, batch, num_heads, num_kv_heads,
+                                  head_dim, scale, max_context_len, workspace, workspace_bytes);
+  if (st != NVAMD_OK) return st;
+  return dispatch_gqa<false>(a, num_heads / num_kv_heads, batch, stream);
+}
+
+extern "C" int nvamd_paged_decode_fused(void *out, int64_t out_stride, const void *q, int64_t q_stride,
+                                        const void *k, int64_t k_stride, const void *v, int64_t v_stride,
+                                        const void *q_weight, const void *k_weight, const int64_t *positions,
+                                        const float *cos_sin, int max_positions, float eps, void *k_cache,
+                                        void *v_cache, int num_blocks, int block_size, const int64_t *slot_mapping,
+                                        const int32_t *block_tables, int bt_stride, int bt_width,
+                                        const int32_t *context_lens, int batch, int num_heads, int num_kv_heads,
+                                        int head_dim, float scale, int max_context_len, void *workspace,
+                                        size_t workspace_bytes, hipStream_t stream) {
+  if (batch == 0) return NVAMD_OK;
+  DecodeArgs a;
+  const int st = fill_decode_args(a, out, out_stride, q, q_stride, k_cache, v_cache, num_blocks, block_size,
+                                  block_tables, bt_stride, bt_width, context_lens, batch, num_heads, num_kv_heads,
+                                  head_dim, scale, max_context_len, workspace, workspace_bytes);
+  if (st != NVAMD_OK) return st;
+  if (!k || !v || !q_weight || !k_weight || !positions || !cos_sin || !slot_mapping || max_positions <= 0)
+    return NVAMD_EINVAL;
+  if (!aligned16(k) || !aligned16(v) || !aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos_sin) ||
+      k_stride % 8 || v_stride % 8 || k_stride < (int64_t)num_kv_heads * head_dim ||
+      v_stride < (int64_t)num_kv_heads * head_dim)
+    return NVAMD_EINVAL;
+  a.k_new = static_cast<const u16 *>(k);
+  a.k_new_stride = k_stride;
+  a.v_new = static_cast<const u16 *>(v);
+  a.v_new_stride = v_stride;
+  a.q_w = static_cast<const u16 *>(q_weight);
+  a.k_w = static_cast<const u16 *>(k_weight);
+  a.positions = positions;
+  a.cos_sin = cos_sin;
+  a.max_positions = max_positions;
+  a.eps = eps;
+  a.slots = slot_mapping;
+  a.num_slots = (int64_t)num_blocks * block_size;
+  return dispatch_gqa<true>(a, num_heads / num_kv_heads, batch, stream);
 }

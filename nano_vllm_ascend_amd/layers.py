@@ -105,6 +105,29 @@ class HipPagedAttention(nn.Module):
                                self.scale, max_context_len, workspace)
 
 
+    def decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm: RMSNorm, k_norm: RMSNorm,
+                    rotary: RotaryEmbedding, positions: torch.Tensor, key_cache: torch.Tensor,
+                    value_cache: torch.Tensor, slot_mapping: torch.Tensor, block_tables: torch.Tensor,
+                    context_lens: torch.Tensor, max_context_len: int | None = None,
+                    workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """One launch for a decode batch: q/k RMSNorm + RoPE, the KV store of post-RoPE k and raw v at
+        slot_mapping, then this attention -- bit-identical to qk_norm_rope followed by forward().
+        q, k, v are the raw projection rows and are left unmodified."""
+        total_tokens, num_heads, head_dim = q.shape
+        if num_heads != self.num_heads or head_dim != self.head_dim:
+            raise ValueError(f"query shape mismatch: got {tuple(q.shape)}")
+        if max_context_len is None:
+            max_context_len = block_tables.shape[1] * key_cache.shape[1]
+        if context_lens.device != q.device:
+            context_lens = context_lens.to(q.device, non_blocking=True)
+        if workspace is None:
+            workspace = self.workspace(total_tokens, max_context_len, q.device)
+        out = torch.empty_like(q) if out is None else out
+        return _C.paged_decode_fused(out, q, k, v, q_norm.weight, k_norm.weight, positions, rotary.cos_sin,
+                                     q_norm.variance_epsilon, key_cache, value_cache, slot_mapping, block_tables,
+                                     context_lens.to(torch.int32), self.scale, max_context_len, workspace)
+
+
 class HipBatchPrefillAttention(nn.Module):
     """Causal varlen prefill; dense route on activations, paged route (any prefix hit) through the cache."""
 

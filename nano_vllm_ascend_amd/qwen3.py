@@ -1,16 +1,18 @@
 """Qwen3 decoder with the HIP attention path (nv/models/qwen3.py:1-221).
 
-Per layer: RMSNorm -> fused qkv projection -> qk_norm_rope (per-head RMSNorm,
-rotate-half RoPE and the KV store of post-RoPE k and raw v, one kernel) ->
-prefill or paged-decode attention -> o_proj -> residual -> RMSNorm -> SwiGLU
-MLP (fused gate/up projection) -> residual.  q/k/v are views into the fused projection
-output, which the kernels accept through their row strides.
+Per layer: RMSNorm -> fused qkv projection -> per-head RMSNorm of q and k, rotate-half
+RoPE and the KV store of post-RoPE k and raw v -> prefill or paged-decode attention ->
+o_proj -> residual -> RMSNorm -> SwiGLU MLP (fused gate/up projection) -> residual.
+Prefill runs the norm/RoPE/store as one kernel (qk_norm_rope) before attention; a decode
+batch runs all of it inside the paged-decode launch (one kernel, identical bits).  q/k/v
+are views into the fused projection output, which the kernels accept through their row
+strides.
 
 Decode batches of <= 32 rows take a fused path (``forward_decode_fused``): the
 skinny-M HIP GEMM runs every projection, each RMSNorm in the prologue of the GEMM
 that consumes it, and each residual add in the epilogue of the GEMM that produces
 it (with the per-32-column sums of squares the next norm needs), and SiLU*mul in
-the gate/up epilogue -- 6 launches per layer instead of 9, same rounding points.
+the gate/up epilogue -- 5 launches per layer instead of 9, same rounding points.
 Prefill and larger batches run the unfused chain on hipBLASLt + add_rms_norm.
 """
 from __future__ import annotations
@@ -56,16 +58,23 @@ class Qwen3Attention(nn.Module):
         q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
-        qk_norm_rope(q, k, v, self.q_norm, self.k_norm, rotary, positions, kv_cache, self.layer_idx,
-                     attn_metadata.slot_mapping)
-        key_cache, value_cache = kv_cache.get_physical_cache(self.layer_idx)
         if is_prefill:
+            qk_norm_rope(q, k, v, self.q_norm, self.k_norm, rotary, positions, kv_cache, self.layer_idx,
+                         attn_metadata.slot_mapping)
+            key_cache, value_cache = kv_cache.get_physical_cache(self.layer_idx)
             attn = self.prefill_attn(q, k, v, attn_metadata, key_cache, value_cache)
         else:
-            attn = self.paged_attn(q, key_cache, value_cache, attn_metadata.block_tables, attn_metadata.context_lens,
-                                   max_context_len=getattr(attn_metadata, "max_context_bound", None),
-                                   workspace=getattr(attn_metadata, "decode_workspace", None))
+            attn = self.decode_attention(q, k, v, rotary, positions, kv_cache, attn_metadata)
         return linear(attn.reshape(t, self.q_size), self.o_weight, skinny=False)
+
+    def decode_attention(self, q, k, v, rotary, positions, kv_cache, attn_metadata):
+        """q/k norms, RoPE, the KV store and paged attention of a decode batch in one launch."""
+        key_cache, value_cache = kv_cache.get_physical_cache(self.layer_idx)
+        return self.paged_attn.decode_step(q, k, v, self.q_norm, self.k_norm, rotary, positions, key_cache,
+                                           value_cache, attn_metadata.slot_mapping, attn_metadata.block_tables,
+                                           attn_metadata.context_lens,
+                                           max_context_len=getattr(attn_metadata, "max_context_bound", None),
+                                           workspace=getattr(attn_metadata, "decode_workspace", None))
 
     def decode_fused(self, residual, ssq, norm: RMSNorm, rotary, positions, kv_cache, attn_metadata, workspace):
         """residual += o_proj(attention(qkv_proj(norm(residual)))) in place, for a decode batch of
@@ -77,12 +86,7 @@ class Qwen3Attention(nn.Module):
         q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
-        qk_norm_rope(q, k, v, self.q_norm, self.k_norm, rotary, positions, kv_cache, self.layer_idx,
-                     attn_metadata.slot_mapping)
-        key_cache, value_cache = kv_cache.get_physical_cache(self.layer_idx)
-        attn = self.paged_attn(q, key_cache, value_cache, attn_metadata.block_tables, attn_metadata.context_lens,
-                               max_context_len=getattr(attn_metadata, "max_context_bound", None),
-                               workspace=getattr(attn_metadata, "decode_workspace", None))
+        attn = self.decode_attention(q, k, v, rotary, positions, kv_cache, attn_metadata)
         _C.skinny_linear(attn.reshape(t, self.q_size), self.o_weight, residual, epilogue=_C.EPI_RESID, y_ssq=ssq,
                          workspace=workspace)
 
@@ -144,7 +148,7 @@ class Qwen3Model(nn.Module):
 
     def forward_decode_fused(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, workspace):
         """Decode forward for <= 32 rows with every RMSNorm and residual add folded into the
-        projections: 6 launches per layer (qkv, qk_norm_rope, attention, o, gate_up, down).
+        projections: 5 launches per layer (qkv, norm/RoPE/store + attention, o, gate_up, down).
         Returns the final residual stream and its per-32-column sums of squares; the final
         norm runs in the LM head's prologue."""
         t = input_ids_flat.shape[0]
