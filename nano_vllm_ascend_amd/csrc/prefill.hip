@@ -10,11 +10,10 @@
 //
 // Workgroup = 4 waves = one kv head g, its GQA query heads, and a tile of
 // BQ = 128/GQA query tokens; wave w owns 32 query rows of one head.  Three
-// workgroups share a CU (three waves per SIMD at <= 168 VGPRs, 3 x 37 KB of
+// workgroups share a CU (three waves per SIMD at <= 168 VGPRs, 3 x 48 KB of
 // LDS), so one wave's softmax and LDS traffic overlap another's MFMAs and the
 // workgroups' per-tile barriers do not hold each other up.  32-key tiles keep
-// both budgets: 64-key tiles (70 KB, 200 VGPRs) allow two workgroups per CU and
-// measure 1.07x slower.
+// both budgets: 64-key tiles allow two workgroups per CU and measured 1.07x slower.
 // Per 32-key tile:
 //   S^T[32 keys x 32 queries] = K . Q^T  with v_mfma_f32_32x32x16_bf16
 //        (A = K rows from LDS, B = Q rows kept in registers for the whole loop).
@@ -23,9 +22,9 @@
 //   O^T[128 dims x 32 queries] += V^T . P^T
 //        The contraction index can be permuted as long as both operands agree:
 //        taking the k-slots in the order the S^T accumulator already holds its
-//        rows makes P^T a register-only repack (no lane movement); V^T is read
-//        from a transposed LDS copy whose keys are stored in that order, one
-//        16-byte read per operand.
+//        rows makes P^T a register-only repack (no lane movement); V^T comes from
+//        the row-major V tile through two transposing LDS reads (ds_read_b64_tr_b16)
+//        per operand, whose source rows pick the keys in that order.
 // Softmax: the running max is kept on raw scores and applied in the exponent's
 // FMA; its reference moves only when a score exceeds it by 2^8 (lazy rescale),
 // and the row sum adds each packed bf16 pair with one v_dot2.
@@ -33,28 +32,22 @@
 // hardware's round-robin over the 8 XCDs puts every query tile of one (sequence, kv
 // head) on one XCD, back to back, heaviest (most keys) first, so they read that head's
 // K/V tiles while the XCD's L2 still holds them (a query-tile-major order streams every
-// sequence's K/V from memory once per tile: 1.3x the time).  K/V tiles are
-// double-buffered in LDS: the next tile is loaded into registers while the current
-// one's MFMAs run, then stored into the other slot, so each tile costs one barrier.
+// sequence's K/V from memory once per tile: 1.3x the time).  K/V tiles go from memory
+// straight into LDS (LDS-DMA, no register staging), three stages deep: tile t+2 loads
+// while tile t is computed, and each tile costs one barrier.  Against register staging
+// with two stages this is equal on the dense route and 1.09x faster on the paged route,
+// whose block-table reads became two scalar loads per tile.
 #include "common.h"
 
 namespace nvamd {
 namespace {
 
 constexpr int kBK = 32;            // keys per tile
-constexpr int kBlocks = kBK / 32;  // 32-key MFMA blocks per tile
-constexpr int kKStride = 136;      // LDS row stride (elements) of the K tile: 272 B, spreads banks
-constexpr int kVtStride = kBK + 8;  // LDS row stride (elements) of the transposed V tile: 16-byte aligned
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 // Largest K/V activation row stride (elements) of the dense route: a 64-row tile's byte range
 // is a 32-bit buffer size.
 constexpr int64_t kMaxActStride = (int64_t)1 << 24;
 constexpr u32 kBf16PairOne = 0x3F803F80u;  // (1.0, 1.0) as a bf16 pair
-
-// Position of key k of a key tile inside a V^T row.  Within each 16-key group the PV
-// step of lane half h consumes keys {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1); swapping
-// bits 2 and 3 of the key makes each of those sets 8 contiguous elements.
-__device__ __forceinline__ int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 struct PrefillArgs {
   u16 *out;
@@ -79,15 +72,34 @@ struct PrefillArgs {
   float scale_log2e;
 };
 
+// 16 bytes per lane into LDS at lds_base + 16 * lane (LDS-DMA), from a raw buffer (range
+// checked: lanes past num_records write zeros) or from a global address.  Issued through asm so
+// the compiler does not track the LDS write and adds no waits of its own: the kernel waits for
+// these loads explicitly (vmcnt counts them) before the barrier that publishes a tile.  One
+// wait state separates the M0 write from its use.
+__device__ __forceinline__ void dma16_buffer(u32x4 rsrc, u32 voffset, u32 lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_global(const void *src, u32 lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_base), "v"(src)
+               : "memory", "m0");
+}
+__device__ __forceinline__ u32 lds_addr(const u16 *p) {
+  return (u32)(uintptr_t)(const __attribute__((address_space(3))) u16 *)p;
+}
+
 __device__ __forceinline__ f32x16 mfma32(bf16x8v a, bf16x8v b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 constexpr int kWaves = 4;  // three workgroups per CU: their barriers are independent
 constexpr int kThreads = kWaves * 64;
-constexpr int kKLoads = kBK * 16 / kThreads;      // 16-byte K chunks per thread per tile
-constexpr int kVLoads = kBK / 2 * 16 / kThreads;  // (key pair, 8-dim chunk) units per thread
-static_assert(kKLoads >= 1 && kVLoads >= 1, "tile staging needs <= 512 threads");
+static_assert(kWaves == 4 && kBK == 32, "the tile DMA maps 4 waves x 8 rows onto a 32-key tile");
 
 template <int GQA, bool PAGED>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
@@ -118,8 +130,9 @@ prefill_kernel(PrefillArgs a) {
   const bool q_ok = rq < q_len;
   const int64_t q_tok = q_start + min(rq, q_len - 1);
 
-  __shared__ __attribute__((aligned(16))) u16 sK[2][kBK][kKStride];
-  __shared__ __attribute__((aligned(16))) u16 sVt[2][D][kVtStride];
+  // Three stages of K and V, row-major with swizzled 16-byte chunks.
+  __shared__ __attribute__((aligned(16))) u16 sK[3][kBK * D];
+  __shared__ __attribute__((aligned(16))) u16 sV[3][kBK * D];
 
   // Q^T operand: lane holds dims 16kk + 8*hl + 0..7 of its query row, kk = 0..7.
   bf16x8v qf[8];
@@ -141,146 +154,142 @@ prefill_kernel(PrefillArgs a) {
   const int n_tiles = ceil_div(kv_hi, kBK);
   const int wave_last_key = offset + min(r0 + 31, q_len - 1);  // beyond: fully masked for this wave
 
-  // cooperative tile loads: K rows (t>>4) + (threads/16)i, 16-byte chunk t&15; V row pair t&31,
-  // 8 dims 8 * ((t>>5) + (threads/32)e)
-  const int kr = tid >> 4, kc = tid & 15;
-  const int vp = tid % (kBK / 2), vc = tid / (kBK / 2);
+  // Tile staging: K and V tiles (32 rows x 256 B each) go from memory straight into LDS with
+  // 16-byte LDS-DMA loads, three stages deep, two tiles ahead of the MFMAs.  A DMA instruction
+  // of wave w fills 4 rows (1 KB): lane l lands at row 4i + l/16 of the wave's 8 rows, 16-byte
+  // slot l%16, and so loads the chunk that slot holds under the row's swizzle.  K rows are
+  // swizzled by row & 15 (the S operand reads 16 consecutive rows at one chunk), V rows by
+  // 2(row & 7) (a transposing read takes 4 consecutive rows x 2 adjacent chunks): both read
+  // patterns then touch distinct banks.  Rows past the sequence read as zeros (dense route:
+  // the buffer range check) or repeat the last key's row (paged route): finite either way.
+  const int dma_row = 8 * w + (lane >> 4);  // + 4i for instruction i
+  const int dma_slot = lane & 15;
+  auto k_chunk = [&](int row) { return dma_slot ^ (row & 15); };
+  auto v_chunk = [&](int row) { return dma_slot ^ (2 * (row & 7)); };
   const int32_t *bt_row = PAGED ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
   const int64_t cache_row = (int64_t)a.num_kv_heads * D;
   const int bs_mask = (1 << a.bs_log2) - 1;
 
-  // Paged route: each row through the block table.  Keys past kv_len re-read the last key's
-  // row (a finite value): their scores are masked to -inf, so they enter P as exact zeros.
-  auto row_ptr = [&](const u16 *cache, int key) -> const u16 * {
-    key = min(key, kv_len - 1);
-    int blk = bt_row[key >> a.bs_log2];
-    blk = min(max(blk, 0), a.num_blocks - 1);
-    return cache + (((int64_t)blk << a.bs_log2) + (key & bs_mask)) * cache_row + (int64_t)g * D;
-  };
   // Dense route: one raw buffer descriptor per tile over the tile's rows of this sequence
-  // (built in scalar registers); every thread's byte offsets inside a tile are constants and
-  // rows past kv_len read as zeros, so a load costs no vector address arithmetic.
-  u32 k_off[kKLoads], v_off[kVLoads][2];
+  // (built in scalar registers); each thread's byte offsets inside a tile are constants.
+  u32 k_off[2], v_off[2];
   if (!PAGED) {
 #pragma unroll
-    for (int i = 0; i < kKLoads; ++i)
-      k_off[i] = (u32)(((kr + kThreads / 16 * i) * a.k_stride + g * D + 8 * kc) * 2);
-#pragma unroll
-    for (int i = 0; i < kVLoads; ++i)
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-        v_off[i][e] = (u32)(((2 * vp + e) * a.v_stride + g * D + 8 * (vc + kThreads / (kBK / 2) * i)) * 2);
+    for (int i = 0; i < 2; ++i) {
+      const int row = dma_row + 4 * i;
+      k_off[i] = (u32)((row * a.k_stride + g * D + 8 * k_chunk(row)) * 2);
+      v_off[i] = (u32)((row * a.v_stride + g * D + 8 * v_chunk(row)) * 2);
+    }
   }
+  // raw buffer descriptor over the tile's rows of this sequence: base, stride 0, byte count
   auto tile_rsrc = [&](const u16 *act, int64_t stride, int t) {
     const int base = t * kBK;
     const int rows = min(kv_len - base, kBK);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<u16 *>(act + (int64_t)(q_start + base) * stride), 0,
-                                             rows * (int)stride * 2, kBufferRsrcWord3);
+    const uint64_t addr = (uint64_t)(uintptr_t)(act + (int64_t)(q_start + base) * stride);
+    return u32x4{(u32)addr, (u32)(addr >> 32) & 0xffffu, (u32)(rows * (int)stride * 2), (u32)kBufferRsrcWord3};
   };
-
-  u32x4 kreg[kKLoads], vreg[kVLoads][2];
-  auto load_k = [&](int t) {
+  auto dma_tile = [&](int t, int st) {
+    const u32 dk = lds_addr(&sK[st][8 * w * D]);
+    const u32 dv = lds_addr(&sV[st][8 * w * D]);
     if (PAGED) {
+      // A 32-key tile spans one block, or two of 16 keys (both entries are scalar loads); each
+      // DMA instruction's 4 rows lie in one 16-row half, so its block, and a buffer descriptor
+      // over that block, are wave-uniform.  Keys past kv_len repeat the last key's row.
+      const int k0 = min(t * kBK, kv_len - 1), k1 = min(t * kBK + 16, kv_len - 1);
+      const int b0 = min(max(bt_row[k0 >> a.bs_log2], 0), a.num_blocks - 1);
+      const int b1 = min(max(bt_row[k1 >> a.bs_log2], 0), a.num_blocks - 1);
+      const u32 block_bytes = (u32)((cache_row << a.bs_log2) * 2);
 #pragma unroll
-      for (int i = 0; i < kKLoads; ++i) kreg[i] = ld16(row_ptr(a.k_cache, t * kBK + kr + kThreads / 16 * i) + 8 * kc);
-    } else {
-      const __amdgpu_buffer_rsrc_t r = tile_rsrc(a.k, a.k_stride, t);
-#pragma unroll
-      for (int i = 0; i < kKLoads; ++i)
-        kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, k_off[i], 0, 0));
-    }
-  };
-  auto load_v = [&](int t) {
-    if (PAGED) {
-#pragma unroll
-      for (int i = 0; i < kVLoads; ++i)
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          vreg[i][e] = ld16(row_ptr(a.v_cache, t * kBK + 2 * vp + e) + 8 * (vc + kThreads / (kBK / 2) * i));
-    } else {
-      const __amdgpu_buffer_rsrc_t r = tile_rsrc(a.v, a.v_stride, t);
-#pragma unroll
-      for (int i = 0; i < kVLoads; ++i)
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          vreg[i][e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, v_off[i][e], 0, 0));
-    }
-  };
-  auto store_k = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < kKLoads; ++i) *reinterpret_cast<u32x4 *>(&sK[slot][kr + kThreads / 16 * i][8 * kc]) = kreg[i];
-  };
-  auto store_v = [&](int slot) {
-    // transpose V: (V[2vp][d], V[2vp+1][d]) -> one dword of row d of V^T, at the permuted
-    // position of key 2vp (keys 2vp and 2vp+1 stay adjacent)
-    const int vpos = vt_pos(2 * vp);
-#pragma unroll
-    for (int i = 0; i < kVLoads; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d = 8 * (vc + kThreads / (kBK / 2) * i) + 2 * e;
-        *reinterpret_cast<u32 *>(&sVt[slot][d][vpos]) = pair_lo(vreg[i][0][e], vreg[i][1][e]);
-        *reinterpret_cast<u32 *>(&sVt[slot][d + 1][vpos]) = pair_hi(vreg[i][0][e], vreg[i][1][e]);
+      for (int i = 0; i < 2; ++i) {
+        const int blk = 8 * w + 4 * i < 16 ? b0 : b1;
+        const int64_t first = ((int64_t)blk << a.bs_log2) * cache_row;
+        const uint64_t ka = (uint64_t)(uintptr_t)(a.k_cache + first), va = (uint64_t)(uintptr_t)(a.v_cache + first);
+        const u32x4 rk = {(u32)ka, (u32)(ka >> 32) & 0xffffu, block_bytes, (u32)kBufferRsrcWord3};
+        const u32x4 rv = {(u32)va, (u32)(va >> 32) & 0xffffu, block_bytes, (u32)kBufferRsrcWord3};
+        const int row = dma_row + 4 * i;
+        const int key = min(t * kBK + row, kv_len - 1);
+        const u32 row_off = (u32)(((key & bs_mask) * cache_row + g * D) * 2);
+        dma16_buffer(rk, row_off + 16 * k_chunk(row), dk + 4 * i * D * 2);
+        dma16_buffer(rv, row_off + 16 * v_chunk(row), dv + 4 * i * D * 2);
       }
-  };
-  // S^T = K Q^T for the keys of a K slot (kBlocks 32-key blocks)
-  auto score = [&](int slot, f32x16 (&st)[kBlocks]) {
+    } else {
+      const u32x4 rk = tile_rsrc(a.k, a.k_stride, t);
+      const u32x4 rv = tile_rsrc(a.v, a.v_stride, t);
 #pragma unroll
-    for (int blk = 0; blk < kBlocks; ++blk) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st[blk][i] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8v kf = *reinterpret_cast<const bf16x8v *>(&sK[slot][32 * blk + n][16 * kk + 8 * hl]);
-        st[blk] = mfma32(kf, qf[kk], st[blk]);
+      for (int i = 0; i < 2; ++i) {
+        dma16_buffer(rk, k_off[i], dk + 4 * i * D * 2);
+        dma16_buffer(rv, v_off[i], dv + 4 * i * D * 2);
       }
     }
+  };
+  // S^T = K Q^T: lane (n, hl) takes dims 16kk + 8hl .. +7 of key row n, chunk 2kk + hl.
+  auto score = [&](const u16 *sk, f32x16 &sc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bf16x8v kf =
+          *reinterpret_cast<const bf16x8v *>(sk + n * D + 8 * ((2 * kk + hl) ^ (n & 15)));
+      sc = mfma32(kf, qf[kk], sc);
+    }
+  };
+  // V^T operand of O^T += V^T P^T for dims 32db.. and the 16 keys of step hh, by two
+  // transposing reads.  In 16-lane group G, output lane i gets dim 32db + 16(G&1) + i of the
+  // 4 rows its source lanes j = q + 4e (e = 0..3) point at, so source lane j points at dims
+  // +4q..+4q+3 of row 16hh + 4hl + e (first read) or + 8 (second read): the k-slots 8hl + 0..7
+  // then hold keys {0-3, 8-11} + 4hl of the step, the order the S^T accumulator gives P^T.
+  const int tr_q = lane & 3, tr_e = (lane >> 2) & 3;
+  auto v_operand = [&](const u16 *sv, int db, int hh) {
+    const int dim = 32 * db + 16 * ((lane >> 4) & 1) + 4 * tr_q;
+    const int r1 = 16 * hh + 4 * hl + tr_e, r2 = r1 + 8;
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4 lds_s4;
+    const u16 *p1 = sv + r1 * D + 8 * ((dim >> 3) ^ (2 * (r1 & 7))) + (dim & 4);
+    const u16 *p2 = sv + r2 * D + 8 * ((dim >> 3) ^ (2 * (r2 & 7))) + (dim & 4);
+    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)p1);
+    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)p2);
+    typedef short s8 __attribute__((ext_vector_type(8)));
+    const s8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8v, both);
   };
   auto visible = [&](int t) { return r0 < q_len && t < n_tiles && t * kBK <= wave_last_key; };
 
-  // Double-buffered tiles: the next tile's K/V are loaded into registers while this tile's
-  // MFMAs run, then stored into the other LDS slot; one barrier per tile.
-  if (n_tiles > 0) {
-    load_k(0);
-    load_v(0);
-    store_k(0);
-    store_v(0);
-  }
-  // Drain every load issued so far (the Q fragments) before the loop.  Otherwise the wait
-  // the compiler places ahead of the first use of Q is kept on every iteration, and each
-  // tile's MFMAs would wait for the next tile's K/V loads issued just before them.
+  // Three stages: tile t+2 is in flight while tile t is computed.  The barrier ending tile t
+  // waits only for tile t+1's DMA (vmcnt counts this wave's 4 DMA instructions per tile; no
+  // other vector memory access is in flight in the loop) and for this wave's LDS reads.
+  if (n_tiles > 0) dma_tile(0, 0);
+  if (n_tiles > 1) dma_tile(1, 1);
+  // Drain the Q fragments and the first two tiles: otherwise the wait the compiler places
+  // ahead of the first use of Q is kept on every iteration.
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
+  // tile t is computed from stage t % 3 while tile t + 2 loads into stage (t + 2) % 3, which
+  // held tile t - 1: every wave finished reading it before the last barrier
   for (int t = 0; t < n_tiles; ++t) {
-    if (t + 1 < n_tiles) {
-      load_k(t + 1);
-      load_v(t + 1);
-    }
+    const u16 *sk = sK[t % 3];
+    const u16 *sv = sV[t % 3];
+    if (t + 2 < n_tiles) dma_tile(t + 2, (t + 2) % 3);
     const int base = t * kBK;
     if (visible(t)) {
-      f32x16 st[kBlocks];
-      score(t & 1, st);
-      // mask; key of register i of block blk: base + 32blk + 8(i/4) + 4hl + i%4.  The running
-      // max is taken on raw scores (scale > 0) and applied in the exponent's FMA.
-      // Only tiles that cross this wave's diagonal or the end of the keys need the mask
-      // (1-2 per wave); the test is wave-uniform, so the others skip it with one branch.
+      f32x16 sc;
+      score(sk, sc);
+      // mask; key of register i: base + 8(i/4) + 4hl + i%4.  The running max is taken on raw
+      // scores (scale > 0) and applied in the exponent's FMA.  Only tiles that cross this
+      // wave's diagonal or the end of the keys need the mask (1-2 per wave); the test is
+      // wave-uniform, so the others skip it with one branch.
       const bool need_mask = (base + kBK - 1 > offset + r0) || (base + kBK > kv_len);
       if (__builtin_expect(need_mask, 0)) {
-        // lane's last visible key, relative to the key of register 0 of block 0
+        // lane's last visible key, relative to the key of register 0
         const int lim = min(offset + rq, kv_len - 1) - base - 4 * hl;
 #pragma unroll
-        for (int blk = 0; blk < kBlocks; ++blk)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (32 * blk + 8 * (i / 4) + (i % 4) > lim) st[blk][i] = -INFINITY;
+        for (int i = 0; i < 16; ++i)
+          if (8 * (i / 4) + (i % 4) > lim) sc[i] = -INFINITY;
       }
       float tmax = -INFINITY;
 #pragma unroll
-      for (int blk = 0; blk < kBlocks; ++blk)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[blk][i]);
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sc[i]);
       tmax = max_xor32(tmax) * a.scale_log2e;
       // Lazy rescale: the exponent's reference moves only when a score exceeds it by more
       // than 2^8, so P <= 256 and O, l are rescaled only on the tiles where some lane's
@@ -292,22 +301,19 @@ prefill_kernel(PrefillArgs a) {
       }
       const float neg_ref = m_run == -INFINITY ? 0.f : -m_run;
       float psum = 0.f;
-      bf16x8v pf[kBlocks][2];
+      bf16x8v pf[2];
 #pragma unroll
-      for (int blk = 0; blk < kBlocks; ++blk)
+      for (int hh = 0; hh < 2; ++hh) {
+        u32x4 packed;
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          u32x4 packed;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const u32 pr =
-                pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(st[blk][8 * hh + 2 * e], a.scale_log2e, neg_ref)),
-                            __builtin_amdgcn_exp2f(fmaf(st[blk][8 * hh + 2 * e + 1], a.scale_log2e, neg_ref)));
-            psum = dot2_bf16(pr, kBf16PairOne, psum);  // both rounded values of the pair
-            packed[e] = pr;
-          }
-          pf[blk][hh] = __builtin_bit_cast(bf16x8v, packed);
+        for (int e = 0; e < 4; ++e) {
+          const u32 pr = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[8 * hh + 2 * e], a.scale_log2e, neg_ref)),
+                                     __builtin_amdgcn_exp2f(fmaf(sc[8 * hh + 2 * e + 1], a.scale_log2e, neg_ref)));
+          psum = dot2_bf16(pr, kBf16PairOne, psum);  // both rounded values of the pair
+          packed[e] = pr;
         }
+        pf[hh] = __builtin_bit_cast(bf16x8v, packed);
+      }
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {  // wave-uniform
         l_run *= alpha;
 #pragma unroll
@@ -317,25 +323,16 @@ prefill_kernel(PrefillArgs a) {
       }
       l_run += psum;
 
-      // O^T += V^T P^T; k-slot 8hl+e of step (blk, hh) is key 32blk + 16hh + 8(e/4) + 4hl + e%4,
-      // which the permuted V^T layout stores contiguously: one 16-byte read per operand.
+      // O^T += V^T P^T, two 16-key steps
 #pragma unroll
-      for (int blk = 0; blk < kBlocks; ++blk)
+      for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int k0 = 32 * blk + 16 * hh + 8 * hl;
-#pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            const u32x4 vv = *reinterpret_cast<const u32x4 *>(&sVt[t & 1][32 * db + n][k0]);
-            acc[db] = mfma32(__builtin_bit_cast(bf16x8v, vv), pf[blk][hh], acc[db]);
-          }
-        }
+        for (int db = 0; db < 4; ++db) acc[db] = mfma32(v_operand(sv, db, hh), pf[hh], acc[db]);
     }
-    if (t + 1 < n_tiles) {  // nobody reads that slot: every wave finished tile t-1 before the last barrier
-      store_k((t + 1) & 1);
-      store_v((t + 1) & 1);
-    }
-    __syncthreads();
+    if (t + 2 < n_tiles)
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 
   // normalise and write: register i of block db is dim 32db + 8(i/4) + 4hl + i%4 of query column n
@@ -418,7 +415,8 @@ extern "C" int nvamd_paged_prefill(void *out, int64_t out_stride, const void *q,
   if (n_seqs == 0 || max_q_len == 0) return NVAMD_OK;
   if (head_dim != kHeadDim) return NVAMD_EUNSUPPORTED;
   const int bs_log2 = log2_exact(block_size);
-  if (bs_log2 < 0) return NVAMD_EUNSUPPORTED;
+  // a 32-key tile spans at most two blocks, and one block's bytes of a layer fit a buffer range
+  if (bs_log2 < 4 || (int64_t)num_kv_heads * head_dim * block_size * 2 > 0x7fffffff) return NVAMD_EUNSUPPORTED;
   if (!(scale > 0.f)) return NVAMD_EINVAL;  // the softmax keeps its running max on raw scores
   if (!check_common(out, out_stride, q, q_stride, num_heads, num_kv_heads) || !k_cache || !v_cache ||
       !block_tables || !cu_seqlens_q || !kv_lens || n_seqs < 0 || max_q_len < 0 || num_blocks <= 0 ||
