@@ -159,13 +159,13 @@ prefill_kernel(PrefillArgs a) {
   // of wave w fills 4 rows (1 KB): lane l lands at row 4i + l/16 of the wave's 8 rows, 16-byte
   // slot l%16, and so loads the chunk that slot holds under the row's swizzle.  K rows are
   // swizzled by row & 15 (the S operand reads 16 consecutive rows at one chunk), V rows by
-  // 2(row & 7) (a transposing read takes 4 consecutive rows x 2 adjacent chunks): both read
-  // patterns then touch distinct banks.  Rows past the sequence read as zeros (dense route:
+  // 4(row & 3) (a transposing read takes 4 consecutive rows x 2 adjacent chunks per 16 lanes,
+  // x 4 chunks per 32): both read patterns then touch distinct banks.  Rows past the sequence read as zeros (dense route:
   // the buffer range check) or repeat the last key's row (paged route): finite either way.
   const int dma_row = 8 * w + (lane >> 4);  // + 4i for instruction i
   const int dma_slot = lane & 15;
   auto k_chunk = [&](int row) { return dma_slot ^ (row & 15); };
-  auto v_chunk = [&](int row) { return dma_slot ^ (2 * (row & 7)); };
+  auto v_chunk = [&](int row) { return dma_slot ^ (4 * (row & 3)); };
   const int32_t *bt_row = PAGED ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
   const int64_t cache_row = (int64_t)a.num_kv_heads * D;
   const int bs_mask = (1 << a.bs_log2) - 1;
@@ -244,8 +244,8 @@ prefill_kernel(PrefillArgs a) {
     const int r1 = 16 * hh + 4 * hl + tr_e, r2 = r1 + 8;
     typedef short s4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s4 lds_s4;
-    const u16 *p1 = sv + r1 * D + 8 * ((dim >> 3) ^ (2 * (r1 & 7))) + (dim & 4);
-    const u16 *p2 = sv + r2 * D + 8 * ((dim >> 3) ^ (2 * (r2 & 7))) + (dim & 4);
+    const u16 *p1 = sv + r1 * D + 8 * ((dim >> 3) ^ (4 * (r1 & 3))) + (dim & 4);
+    const u16 *p2 = sv + r2 * D + 8 * ((dim >> 3) ^ (4 * (r2 & 3))) + (dim & 4);
     const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)p1);
     const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)p2);
     typedef short s8 __attribute__((ext_vector_type(8)));
