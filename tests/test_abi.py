@@ -48,3 +48,42 @@ def test_build_rejects_kernels_that_spill_to_scratch():
     ])
     assert scratch_by_kernel(remarks) == {"_Z3fooPf": 116, "_Z3barPf": 0}
     assert scratch_by_kernel("") == {}
+
+
+# Argument checks run on the host before any HIP call, so they are testable without a GPU.  The
+# addresses below are fake 16-byte-aligned device addresses that no failing call dereferences.
+EINVAL, EUNSUPPORTED, EWORKSPACE = -1, -2, -3
+A = 0x10000  # aligned stand-in address
+
+
+def _fused(lib, **over):
+    args = dict(out=A, out_stride=2048, q=A, q_stride=4096, k=A, k_stride=4096, v=A, v_stride=4096, qw=A, kw=A,
+                positions=A, cos_sin=A, max_positions=4096, eps=1e-6, k_cache=A, v_cache=A, num_blocks=64,
+                block_size=128, slots=A, bt=A, bt_stride=8, bt_width=8, ctx=A, batch=4, hq=16, hkv=8, d=128,
+                scale=128 ** -0.5, max_ctx=1024, ws=A, ws_bytes=1 << 24, stream=None)
+    args.update(over)
+    return lib.nvamd_paged_decode_fused(*args.values())
+
+
+def test_fused_decode_step_argument_errors():
+    lib = _C.load()
+    assert _fused(lib, batch=0) == 0                       # nothing to do
+    assert _fused(lib, d=64) == EUNSUPPORTED               # head_dim must be 128
+    assert _fused(lib, block_size=8) == EUNSUPPORTED       # block_size >= 16
+    assert _fused(lib, hq=12) == EINVAL                    # Hq not a multiple of Hkv
+    assert _fused(lib, k=A + 2) == EINVAL                  # misaligned new-token rows
+    assert _fused(lib, k_stride=8 * 128 - 8) == EINVAL     # rows shorter than Hkv * D
+    assert _fused(lib, cos_sin=A + 4) == EINVAL            # the rope table is read 16 bytes at a time
+    assert _fused(lib, positions=0) == EINVAL
+    assert _fused(lib, slots=0) == EINVAL
+    assert _fused(lib, max_positions=0) == EINVAL
+    assert _fused(lib, ws_bytes=16) == EWORKSPACE
+
+
+def test_paged_prefill_rejects_small_blocks():
+    lib = _C.load()
+    common = dict(out=A, out_stride=2048, q=A, q_stride=2048, k_cache=A, v_cache=A, num_blocks=64)
+    tail = dict(bt=A, bt_stride=8, bt_width=8, cu=A, kv=A, n_seqs=2, max_q=64, hq=16, hkv=8, d=128,
+                scale=128 ** -0.5, stream=None)
+    for bs, want in ((8, EUNSUPPORTED), (12, EUNSUPPORTED)):
+        assert lib.nvamd_paged_prefill(*common.values(), bs, *tail.values()) == want
