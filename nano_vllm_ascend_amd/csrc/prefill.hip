@@ -44,7 +44,7 @@ namespace {
 
 constexpr int kBK = 32;            // keys per tile
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
-// Largest K/V activation row stride (elements) of the dense route: a 64-row tile's byte range
+// Largest K/V activation row stride (elements) of the dense route: a 32-row tile's byte range
 // is a 32-bit buffer size.
 constexpr int64_t kMaxActStride = (int64_t)1 << 24;
 constexpr u32 kBf16PairOne = 0x3F803F80u;  // (1.0, 1.0) as a bf16 pair
