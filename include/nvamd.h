@@ -131,6 +131,8 @@ int nvamd_kv_cache_write(const void *k, int64_t k_stride,
 /* normed value rounded to bf16, cos/sin rounded to bf16, rotation in fp32    */
 /* with one final rounding.                                                   */
 /* Pass k_cache = v_cache = NULL to skip the store (slot_mapping unused).     */
+/* q, k, v, the weights, cos_sin and the caches: 16-byte aligned, row strides */
+/* multiples of 8 elements (every access is 16 bytes).                        */
 /* ------------------------------------------------------------------------- */
 int nvamd_qk_norm_rope(void *q, int64_t q_stride,
                        void *k, int64_t k_stride,

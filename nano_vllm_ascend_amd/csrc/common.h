@@ -106,6 +106,45 @@ __device__ __forceinline__ float sum8(float v) {
   v += dpp<kDppHalfMirror>(v);
   return v;
 }
+// Per-head RMSNorm + RoPE of one head vector held by an aligned group of 8 lanes: lane c of the
+// group holds dims 8c..8c+7 (lo) and 64+8c..64+8c+7 (hi).  cs/sn are the bf16-rounded cos/sin
+// of dims 8c..8c+7.  A lane forms the partial sums of squares of the dim quads (d, d+1, 64+d,
+// 65+d) it holds, pairs them, and the 8-lane reduction finishes a balanced tree over the 32 quads
+// in order of d, so every kernel that uses it rounds identically.
+__device__ __forceinline__ void head_norm_rope(u32x4 &lo, u32x4 &hi, const u32x4 w_lo, const u32x4 w_hi,
+                                               const float (&cs)[8], const float (&sn)[8], float eps) {
+  float p[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) p[e] = head_ssq4(bf16_lo(lo[e]), bf16_hi(lo[e]), bf16_lo(hi[e]), bf16_hi(hi[e]));
+  const float rstd = head_rstd(sum8((p[0] + p[1]) + (p[2] + p[3])), eps);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float y0 = head_norm(bf16_lo(lo[e]), rstd, bf16_lo(w_lo[e]));
+    const float y1 = head_norm(bf16_hi(lo[e]), rstd, bf16_hi(w_lo[e]));
+    const float y2 = head_norm(bf16_lo(hi[e]), rstd, bf16_lo(w_hi[e]));
+    const float y3 = head_norm(bf16_hi(hi[e]), rstd, bf16_hi(w_hi[e]));
+    const float c0 = cs[2 * e], c1 = cs[2 * e + 1], s0 = sn[2 * e], s1 = sn[2 * e + 1];
+    lo[e] = pack_bf16x2(rope_lo(y0, y2, c0, s0), rope_lo(y1, y3, c1, s1));
+    hi[e] = pack_bf16x2(rope_hi(y0, y2, c0, s0), rope_hi(y1, y3, c1, s1));
+  }
+}
+
+
+// The bf16-rounded cos (cs) and sin (sn) of dims 8c..8c+7 at table row pos: the fp32 table holds
+// 64 cos then 64 sin values per position (nv/layers/rotary_embedding.py:20-42 casts both to bf16).
+__device__ __forceinline__ void rope_row8(const float *cos_sin, int64_t pos, int c, float (&cs)[8], float (&sn)[8]) {
+  const float *row = cos_sin + pos * kHeadDim + 8 * c;
+  const f32x4 c0 = *reinterpret_cast<const f32x4 *>(row), c1 = *reinterpret_cast<const f32x4 *>(row + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4 *>(row + 64), s1 = *reinterpret_cast<const f32x4 *>(row + 68);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    cs[e] = round_bf16(c0[e]);
+    cs[4 + e] = round_bf16(c1[e]);
+    sn[e] = round_bf16(s0[e]);
+    sn[4 + e] = round_bf16(s1[e]);
+  }
+}
+
 // Sum over 16 lanes (one DPP row).
 __device__ __forceinline__ float sum16(float v) {
   v += dpp<kDppQuadXor1>(v);

@@ -5,8 +5,8 @@
 // qk_norm_rope    replaces q_norm/k_norm + apply_rotary_pos_emb_tnd + kv_cache.write
 //   as composed in Qwen3Attention.forward (nv/models/qwen3.py:83-96).
 //
-// Both are pure HBM streams: every byte is read once and written once, with
-// 16-byte (store) / 128-byte-per-32-lanes (norm) coalesced accesses.
+// Both are pure HBM streams: every byte is read once and written once, with 16-byte
+// accesses (eight lanes cover one 256-byte head row in two 128-byte halves).
 #include "common.h"
 
 namespace nvamd {
@@ -55,21 +55,21 @@ struct NormRopeArgs {
   float eps;
 };
 
-// A half-wave (32 lanes) owns one head vector of one token.  Lane l holds dims
-// (2l, 2l+1) and their rotate-half partners (64+2l, 65+2l), so RoPE needs no
-// cross-lane traffic and each 32-lane load covers one 128-byte line.
-// Vectors per token: num_heads q heads, num_kv_heads k heads, then (when a
-// cache is given) num_kv_heads v heads that are only stored.
+// An aligned group of 8 lanes owns one head vector of one token: lane c holds dims
+// 8c..8c+7 and their rotate-half partners 64+8c..64+8c+7, so RoPE needs no lane exchange,
+// every access is 16 bytes, and the norm's sum of squares is an 8-lane reduction
+// (head_norm_rope, shared with the fused decode kernel, so both round identically).
+// Vectors per token: num_heads q heads, num_kv_heads k heads, then (when a cache is given)
+// num_kv_heads v heads that are only stored.  A 256-thread workgroup takes 32 vectors.
 __global__ void __launch_bounds__(256)
 qk_norm_rope_kernel(NormRopeArgs a) {
   const bool store = a.k_cache != nullptr;
   const int vecs = a.num_heads + a.num_kv_heads * (store ? 2 : 1);
-  const int64_t hw = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (hw >= (int64_t)a.num_tokens * vecs) return;
-  const int t = (int)(hw / vecs);
-  const int vec = (int)(hw % vecs);
-  const int l = threadIdx.x & 31;
-  const int d0 = 2 * l;
+  const int64_t gv = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  if (gv >= (int64_t)a.num_tokens * vecs) return;  // whole 8-lane groups leave together
+  const int t = (int)(gv / vecs);
+  const int vec = (int)(gv % vecs);
+  const int c = threadIdx.x & 7;
 
   int64_t slot = -1;
   if (store) {
@@ -81,51 +81,31 @@ qk_norm_rope_kernel(NormRopeArgs a) {
   if (vec >= a.num_heads + a.num_kv_heads) {  // raw V -> cache
     const int h = vec - a.num_heads - a.num_kv_heads;
     if (slot < 0) return;
-    const u16 *src = a.v + (int64_t)t * a.v_stride + h * kHeadDim;
-    u16 *dst = a.v_cache + cache_row + h * kHeadDim;
-    const u32 lo = *reinterpret_cast<const u32 *>(src + d0);
-    const u32 hi = *reinterpret_cast<const u32 *>(src + 64 + d0);
-    *reinterpret_cast<u32 *>(dst + d0) = lo;
-    *reinterpret_cast<u32 *>(dst + 64 + d0) = hi;
+    const u16 *src = a.v + (int64_t)t * a.v_stride + h * kHeadDim + 8 * c;
+    u16 *dst = a.v_cache + cache_row + h * kHeadDim + 8 * c;
+    const u32x4 lo = ld16(src), hi = ld16(src + 64);
+    __builtin_nontemporal_store(lo, reinterpret_cast<u32x4 *>(dst));
+    __builtin_nontemporal_store(hi, reinterpret_cast<u32x4 *>(dst + 64));
     return;
   }
 
   const bool is_q = vec < a.num_heads;
   const int h = is_q ? vec : vec - a.num_heads;
-  u16 *x = is_q ? a.q + (int64_t)t * a.q_stride + h * kHeadDim : a.k + (int64_t)t * a.k_stride + h * kHeadDim;
-  const u16 *wt = is_q ? a.q_w : a.k_w;
-
-  const u32 x_lo = *reinterpret_cast<const u32 *>(x + d0);       // dims d0, d0+1
-  const u32 x_hi = *reinterpret_cast<const u32 *>(x + 64 + d0);  // dims 64+d0, 65+d0
-  const u32 w_lo = *reinterpret_cast<const u32 *>(wt + d0);
-  const u32 w_hi = *reinterpret_cast<const u32 *>(wt + 64 + d0);
-  const float x0 = bf16_lo(x_lo), x1 = bf16_hi(x_lo), x2 = bf16_lo(x_hi), x3 = bf16_hi(x_hi);
-
-  float ss = head_ssq4(x0, x1, x2, x3);
-  ss = sum16(ss);
-  ss += swizzle_xor16(ss);  // the 32 lanes of this half-wave: a balanced tree in lane order
-  const float rstd = head_rstd(ss, a.eps);
-
-  // RMSNorm output rounded to bf16 (the reference's norm returns bf16).
-  const float y0 = head_norm(x0, rstd, bf16_lo(w_lo));
-  const float y1 = head_norm(x1, rstd, bf16_hi(w_lo));
-  const float y2 = head_norm(x2, rstd, bf16_lo(w_hi));
-  const float y3 = head_norm(x3, rstd, bf16_hi(w_hi));
-
+  u16 *x = (is_q ? a.q + (int64_t)t * a.q_stride : a.k + (int64_t)t * a.k_stride) + h * kHeadDim + 8 * c;
+  const u16 *wt = (is_q ? a.q_w : a.k_w) + 8 * c;
+  u32x4 lo = ld16(x), hi = ld16(x + 64);
+  const u32x4 w_lo = ld16(wt), w_hi = ld16(wt + 64);
   int64_t pos = a.positions[t];
   pos = pos < 0 ? 0 : (pos >= a.max_positions ? a.max_positions - 1 : pos);
-  const float *cs = a.cos_sin + pos * kHeadDim;
-  const float c0 = round_bf16(cs[d0]), c1 = round_bf16(cs[d0 + 1]);
-  const float s0 = round_bf16(cs[64 + d0]), s1 = round_bf16(cs[64 + d0 + 1]);
-
-  const u32 o_lo = pack_bf16x2(rope_lo(y0, y2, c0, s0), rope_lo(y1, y3, c1, s1));
-  const u32 o_hi = pack_bf16x2(rope_hi(y0, y2, c0, s0), rope_hi(y1, y3, c1, s1));
-  *reinterpret_cast<u32 *>(x + d0) = o_lo;
-  *reinterpret_cast<u32 *>(x + 64 + d0) = o_hi;
-  if (!is_q && slot >= 0) {
-    u16 *dst = a.k_cache + cache_row + h * kHeadDim;
-    *reinterpret_cast<u32 *>(dst + d0) = o_lo;
-    *reinterpret_cast<u32 *>(dst + 64 + d0) = o_hi;
+  float cs[8], sn[8];
+  rope_row8(a.cos_sin, pos, c, cs, sn);
+  head_norm_rope(lo, hi, w_lo, w_hi, cs, sn, a.eps);
+  st16(x, lo);
+  st16(x + 64, hi);
+  if (!is_q && slot >= 0) {  // post-RoPE k into the cache; not read again by this step
+    u16 *dst = a.k_cache + cache_row + h * kHeadDim + 8 * c;
+    __builtin_nontemporal_store(lo, reinterpret_cast<u32x4 *>(dst));
+    __builtin_nontemporal_store(hi, reinterpret_cast<u32x4 *>(dst + 64));
   }
 }
 
@@ -166,11 +146,13 @@ extern "C" int nvamd_qk_norm_rope(void *q, int64_t q_stride, void *k, int64_t k_
   if (head_dim != kHeadDim) return NVAMD_EUNSUPPORTED;
   const bool store = k_cache != nullptr || v_cache != nullptr;
   if (store && (!k_cache || !v_cache || !v || !slot_mapping || num_slots <= 0)) return NVAMD_EINVAL;
-  auto a4 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; };
-  if (!a4(q) || !a4(k) || !a4(q_weight) || !a4(k_weight) || q_stride % 2 || k_stride % 2 ||
-      q_stride < (int64_t)num_heads * head_dim || k_stride < (int64_t)num_kv_heads * head_dim)
+  // 16-byte accesses: rows, weights, the rope table and the caches 16-byte aligned
+  if (!aligned16(q) || !aligned16(k) || !aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos_sin) ||
+      q_stride % 8 || k_stride % 8 || q_stride < (int64_t)num_heads * head_dim ||
+      k_stride < (int64_t)num_kv_heads * head_dim)
     return NVAMD_EINVAL;
-  if (store && (!a4(v) || !a4(k_cache) || !a4(v_cache) || v_stride % 2 || v_stride < (int64_t)num_kv_heads * head_dim))
+  if (store && (!aligned16(v) || !aligned16(k_cache) || !aligned16(v_cache) || v_stride % 8 ||
+                v_stride < (int64_t)num_kv_heads * head_dim))
     return NVAMD_EINVAL;
 
   NormRopeArgs a;
@@ -194,7 +176,7 @@ extern "C" int nvamd_qk_norm_rope(void *q, int64_t q_stride, void *k, int64_t k_
   a.num_kv_heads = num_kv_heads;
   a.eps = eps;
   const int vecs = num_heads + num_kv_heads * (store ? 2 : 1);
-  const int64_t blocks = ((int64_t)num_tokens * vecs + 7) / 8;
+  const int64_t blocks = ((int64_t)num_tokens * vecs + 31) / 32;
   if (blocks > 0x7fffffff) return NVAMD_EINVAL;
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
   return launch_status();

@@ -99,29 +99,6 @@ struct KVTile {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Per-head RMSNorm + RoPE of one head vector held in this kernel's lane layout: the 8 lanes of a
-// row group hold dims 8c..8c+7 (lo) and 64+8c..64+8c+7 (hi).  cs/sn are the bf16-rounded cos/sin
-// of dims 8c..8c+7.  A lane forms the partial sums of squares of the dim quads (d, d+1, 64+d,
-// 65+d) it holds, pairs them, and the 8-lane reduction finishes the same balanced tree over the
-// 32 quads that the standalone norm kernel computes, so both give identical bits.
-__device__ __forceinline__ void head_norm_rope(u32x4 &lo, u32x4 &hi, const u32x4 w_lo, const u32x4 w_hi,
-                                               const float (&cs)[8], const float (&sn)[8], float eps) {
-  float p[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) p[e] = head_ssq4(bf16_lo(lo[e]), bf16_hi(lo[e]), bf16_lo(hi[e]), bf16_hi(hi[e]));
-  const float rstd = head_rstd(sum8((p[0] + p[1]) + (p[2] + p[3])), eps);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float y0 = head_norm(bf16_lo(lo[e]), rstd, bf16_lo(w_lo[e]));
-    const float y1 = head_norm(bf16_hi(lo[e]), rstd, bf16_hi(w_lo[e]));
-    const float y2 = head_norm(bf16_lo(hi[e]), rstd, bf16_lo(w_hi[e]));
-    const float y3 = head_norm(bf16_hi(hi[e]), rstd, bf16_hi(w_hi[e]));
-    const float c0 = cs[2 * e], c1 = cs[2 * e + 1], s0 = sn[2 * e], s1 = sn[2 * e + 1];
-    lo[e] = pack_bf16x2(rope_lo(y0, y2, c0, s0), rope_lo(y1, y3, c1, s1));
-    hi[e] = pack_bf16x2(rope_hi(y0, y2, c0, s0), rope_hi(y1, y3, c1, s1));
-  }
-}
-
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
