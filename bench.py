@@ -291,6 +291,34 @@ def prefill_leg(args, device) -> dict:
     # ~20 launches (8 ms) of sustained MFMA work pass before the clocks settle
     us_attn = timed(lambda: _C.varlen_prefill(out, q, k, v, cu, max(lens), scale), 40, warmup=30)
     us_store = timed(lambda: _C.kv_cache_write(k, v, kc, vc, slots), 40)
+
+    # per-head q/k RMSNorm + RoPE + KV store of the same tokens, on views into a fused
+    # projection output [T, (16 + 2 * 8) * 128], in place
+    from nano_vllm_ascend_amd.layers import RotaryEmbedding
+
+    table = RotaryEmbedding(128, 40960, W.ROPE_THETA).cos_sin.to(device)
+    qkv = torch.randn(t, 32 * 128, generator=gen, device=device).bfloat16()
+    qv, kv_, vv = qkv[:, :2048].view(t, 16, 128), qkv[:, 2048:3072].view(t, 8, 128), qkv[:, 3072:].view(t, 8, 128)
+    qw = (1.0 + 0.02 * torch.randn(128, generator=gen, device=device)).bfloat16()
+    kw = (1.0 + 0.02 * torch.randn(128, generator=gen, device=device)).bfloat16()
+    pos = torch.tensor([p for n in lens for p in range(n)], dtype=torch.int64, device=device)
+    us_norm = timed(lambda: _C.qk_norm_rope(qv, kv_, qw, kw, pos, table, W.RMS_EPS, v=vv, key_cache=kc,
+                                            value_cache=vc, slot_mapping=slots), 40)
+    norm_bytes = t * ((16 + 8) * 128 * 2 * 2 + 8 * 128 * 2 + 2 * 8 * 128 * 2 + 16)
+
+    # paged (prefix-hit) route: 32 prompts of 1024 cached + 1024 new tokens through block tables
+    pb, pq, pkv = 32, 1024, 2048
+    pblocks = pb * (pkv // 128) + 16
+    pkc = torch.randn(pblocks, 128, 8, 128, generator=gen, device=device).bfloat16()
+    pvc = torch.randn(pblocks, 128, 8, 128, generator=gen, device=device).bfloat16()
+    pbt = torch.randperm(pblocks, generator=torch.Generator().manual_seed(args.seed))[: pb * (pkv // 128)]
+    pbt = pbt.view(pb, pkv // 128).to(torch.int32).to(device)
+    pqq = torch.randn(pb * pq, 16, 128, generator=gen, device=device).bfloat16()
+    pcu = torch.tensor([i * pq for i in range(pb + 1)], dtype=torch.int32, device=device)
+    pkl = torch.full((pb,), pkv, dtype=torch.int32, device=device)
+    pout = torch.empty_like(pqq)
+    us_paged = timed(lambda: _C.paged_prefill(pout, pqq, pkc, pvc, pbt, pcu, pkl, pq, scale), 40, warmup=30)
+    paged_flops = W.causal_attention_flops([pq] * pb, [pkv] * pb, 16)
     flops = W.causal_attention_flops(lens, lens, 16)
     store_bytes = t * 8 * 128 * 2 * 2 * 2 + t * 8  # K and V read + written, slot ids
     tflops = flops / us_attn / 1e6
@@ -303,7 +331,61 @@ def prefill_leg(args, device) -> dict:
         "kv_store": {"kernel": "kv_cache_write_kernel", "us": round(us_store, 2), "bytes": store_bytes,
                      "gbs": round(store_bytes / us_store / 1e3, 1),
                      "frac": round(store_bytes / us_store / 1e3 / HBM_PEAK_GBS, 4)},
+        "qk_norm_rope": {"kernel": "qk_norm_rope_kernel (with the KV store)", "us": round(us_norm, 2),
+                         "bytes": norm_bytes, "gbs": round(norm_bytes / us_norm / 1e3, 1),
+                         "frac": round(norm_bytes / us_norm / 1e3 / HBM_PEAK_GBS, 4)},
+        "paged_route": {"workload": "32 prompts x (1024 cached + 1024 new tokens), block_size 128",
+                        "kernel": "prefill_kernel (paged)", "us": round(us_paged, 2), "flops": paged_flops,
+                        "tflops": round(paged_flops / us_paged / 1e6, 1),
+                        "frac": round(paged_flops / us_paged / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)},
     }
+
+
+def pack_leg(args, device) -> dict:
+    """GPU packing of the batch metadata (slot_mapping, block_tables, context_lens, cu_seqlens,
+    positions, input ids) by BlockManager: a ragged prefill of 32 prompts of U[64, 2048] tokens
+    (token ids included) and a 32-row decode step, block_size 128.  Wall time per call with the
+    host work, the one upload and the kernel, synchronised."""
+    import random
+
+    import torch
+
+    from nano_vllm_ascend_amd import workloads as W
+    from nano_vllm_ascend_amd.block_manager import BlockManager
+
+    lens = W.prefill_lengths(32, 64, 2048, seed=args.seed)
+    rng = random.Random(args.seed)
+    tokens = [[rng.randint(0, 151935) for _ in range(n)] for n in lens]
+    bm = BlockManager(num_blocks=1024, block_size=128, device=device)
+    slots = list(range(32))
+
+    def prefill():
+        bm.prepare_prefill_metadata(slots, lens, [0] * 32, [[] for _ in slots], token_ids=tokens)
+        torch.cuda.synchronize()
+
+    def median_us(fn, reset=None, reps=20):
+        times = []
+        for i in range(reps + 3):
+            t0 = time.perf_counter()
+            fn()
+            dt = time.perf_counter() - t0
+            if reset is not None:
+                reset()
+            if i >= 3:
+                times.append(dt)
+        return sorted(times)[len(times) // 2] * 1e6
+
+    def release():
+        for s_ in slots:
+            bm.free_slot(s_)
+
+    us_prefill = median_us(prefill, reset=release)
+    prefill()
+    decode = lambda: (bm.prepare_decode_metadata(slots, list(lens), 1), torch.cuda.synchronize())
+    us_decode = median_us(decode)
+    return {"prefill_32_prompts_us": round(us_prefill, 1), "tokens": sum(lens),
+            "decode_32_rows_us": round(us_decode, 1),
+            "note": "wall time per call: host descriptors, one upload, pack kernel, synchronise"}
 
 
 def cpu_baseline(work, seconds: float):
@@ -356,6 +438,7 @@ def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 2) -> dict:
 
     from nano_vllm_ascend_amd import workloads as W
     from oracle.attention_ref import paged_decode_ref, varlen_prefill_ref
+    from oracle.block_manager_ref import BlockManagerRef
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -383,10 +466,23 @@ def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 2) -> dict:
     for _ in range(prefill_reps):
         varlen_prefill_ref(pq, pk, pv, cu, scale)
     pf_s = (time.perf_counter() - t0) / prefill_reps
+    # reference-style packing: the per-token slot loop on the host
+    bm = BlockManagerRef(1024, 128)
+    slots = list(range(32))
+    pack_times = []
+    for i in range(8):
+        t0 = time.perf_counter()
+        bm.prepare_prefill_metadata(slots, lens, [0] * 32, [[] for _ in slots])
+        pack_times.append(time.perf_counter() - t0)
+        for s_ in slots:
+            bm.free_slot(s_)
+    pack_s = sorted(pack_times[3:])[2]
     return {
         "cores": cores, "kind": "port",
         "decode_4seq": {"us": round(dec_s * 1e6, 1), "gbs": round(nbytes / dec_s / 1e9, 2),
                         "sample": "fp32 torch-CPU oracle, layer 0, median of 20 after 3 warm-ups"},
+        "pack_prefill_32_prompts": {"us": round(pack_s * 1e6, 1), "tokens": t,
+                                    "sample": "oracle block manager (per-token slot loop), median of 5"},
         "prefill_32xU64-2048": {"ms": round(pf_s * 1e3, 1),
                                 "tflops": round(W.causal_attention_flops(lens, lens, 16) / pf_s / 1e12, 3),
                                 "sample": f"fp32 torch-CPU oracle, {prefill_reps} reps (bounded sample)"},
@@ -454,6 +550,7 @@ def main():
         },
     }
     result["fused_step"] = fused_step_leg(args, dec["work"], device)
+    result["pack"] = pack_leg(args, device)
     small = small_decode_leg(args, device)
     result["decode_small"] = {k: v for k, v in small.items() if k != "work"}
     if not args.no_cpu:
