@@ -195,9 +195,14 @@ prefill_kernel(PrefillArgs a) {
       // A 32-key tile spans one block, or two of 16 keys (both entries are scalar loads); each
       // DMA instruction's 4 rows lie in one 16-row half, so its block, and a buffer descriptor
       // over that block, are wave-uniform.  Keys past kv_len repeat the last key's row.
+      // The table does not change during the launch: read through the constant address space,
+      // the loads stay scalar (the barrier's memory clobber would otherwise make them vector
+      // loads, whose waits the compiler cannot separate from the DMA in flight).
       const int k0 = min(t * kBK, kv_len - 1), k1 = min(t * kBK + 16, kv_len - 1);
-      const int b0 = min(max(bt_row[k0 >> a.bs_log2], 0), a.num_blocks - 1);
-      const int b1 = min(max(bt_row[k1 >> a.bs_log2], 0), a.num_blocks - 1);
+      typedef const __attribute__((address_space(4))) int32_t const_i32;
+      const_i32 *btc = (const_i32 *)bt_row;
+      const int b0 = min(max(btc[k0 >> a.bs_log2], 0), a.num_blocks - 1);
+      const int b1 = min(max(btc[k1 >> a.bs_log2], 0), a.num_blocks - 1);
       const u32 block_bytes = (u32)((cache_row << a.bs_log2) * 2);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
