@@ -393,8 +393,11 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
   a.partials = workspace ? reinterpret_cast<float *>(static_cast<char *>(workspace) + kCounterBytes) : nullptr;
   const int grid = groups * p.ks;
   switch (epilogue) {
-    case kEpiSilu: return norm ? dispatch<kEpiSilu, true>(a, p, grid, stream) : dispatch<kEpiSilu, false>(a, p, grid, stream);
-    case kEpiResid: return norm ? dispatch<kEpiResid, true>(a, p, grid, stream) : dispatch<kEpiResid, false>(a, p, grid, stream);
-    default: return norm ? dispatch<kEpiStore, true>(a, p, grid, stream) : dispatch<kEpiStore, false>(a, p, grid, stream);
+    case kEpiSilu:
+      return norm ? dispatch<kEpiSilu, true>(a, p, grid, stream) : dispatch<kEpiSilu, false>(a, p, grid, stream);
+    case kEpiResid:
+      return norm ? dispatch<kEpiResid, true>(a, p, grid, stream) : dispatch<kEpiResid, false>(a, p, grid, stream);
+    default:
+      return norm ? dispatch<kEpiStore, true>(a, p, grid, stream) : dispatch<kEpiStore, false>(a, p, grid, stream);
   }
 }

@@ -160,8 +160,9 @@ prefill_kernel(PrefillArgs a) {
   // slot l%16, and so loads the chunk that slot holds under the row's swizzle.  K rows are
   // swizzled by row & 15 (the S operand reads 16 consecutive rows at one chunk), V rows by
   // 4(row & 3) (a transposing read takes 4 consecutive rows x 2 adjacent chunks per 16 lanes,
-  // x 4 chunks per 32): both read patterns then touch distinct banks.  Rows past the sequence read as zeros (dense route:
-  // the buffer range check) or repeat the last key's row (paged route): finite either way.
+  // x 4 chunks per 32): both read patterns then touch distinct banks.  Rows past the sequence
+  // read as zeros (dense route: the buffer range check) or repeat the last key's row (paged
+  // route): finite either way.
   const int dma_row = 8 * w + (lane >> 4);  // + 4i for instruction i
   const int dma_slot = lane & 15;
   auto k_chunk = [&](int row) { return dma_slot ^ (row & 15); };
