@@ -76,7 +76,9 @@ struct PrefillArgs {
 // checked: lanes past num_records write zeros) or from a global address.  Issued through asm so
 // the compiler does not track the LDS write and adds no waits of its own: the kernel waits for
 // these loads explicitly (vmcnt counts them) before the barrier that publishes a tile.  One
-// wait state separates the M0 write from its use.
+// wait state separates the M0 write from its use.  hipcc warns that a clobbered M0 may not be
+// preserved: in this kernel's gfx950 code M0 is written only by these statements and read by
+// nothing else, so no live value is lost.
 __device__ __forceinline__ void dma16_buffer(u32x4 rsrc, u32 voffset, u32 lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
