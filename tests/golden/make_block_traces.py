@@ -1,7 +1,7 @@
 """Write tests/golden/block_traces.json from the reference's own Python source.
 
-Run in the development container only (it reads the reference tree, which
-does not exist on the GPU box):  python tests/golden/make_block_traces.py
+Run only where the reference tree is present (the tests read the committed
+JSON, never the reference):  python tests/golden/make_block_traces.py
 
 It imports the reference's pure-Python BlockManager, MiniScheduler,
 EngineCore, Sequence and SamplingParams (they import torch, math and
