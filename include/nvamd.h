@@ -38,7 +38,7 @@ extern "C" {
 
 /* ABI version of this header; nvamd_version() returns the version the library was built
    with, for the loader's sanity check. */
-#define NVAMD_ABI_VERSION 1
+#define NVAMD_ABI_VERSION 2
 int nvamd_version(void);
 
 /* ------------------------------------------------------------------------- */
@@ -243,6 +243,17 @@ int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
 /*   nv/layers/embed_head.py:24-39), with the residual add + RMSNorm of the   */
 /*   decoder layer (nv/models/qwen3.py:138-150, nv/layers/layernorm.py:12-17) */
 /*   folded into the GEMMs on either side of it.                              */
+/* Tiled layout: a [R, C] bf16 matrix (R % 16 == 0, C % 32 == 0) stored as    */
+/*   (R/16) x (C/32) tiles of 16 rows x 32 columns, 512 elements each, in     */
+/*   row-tile-major order; element (r, c) of a tile at                        */
+/*   128 * (c / 8) + 8 * r + c % 8 -- the MFMA operand order, so a wave loads */
+/*   1 KB of contiguous memory per instruction.  Index of element (r, c):     */
+/*   ((r/16) * (C/32) + c/32) * 512 + 128 * ((c%32)/8) + 8 * (r%16) + c%8.    */
+/* w_tiled: the weight [n, k] (epilogue 1: [2n, k]) in tiled layout, no       */
+/*   stride.  flags: NVAMD_GEMM_X_TILED -- x is tiled with 16 * ceil(m/16)    */
+/*   rows (x_stride unused; rows past m only reach dropped outputs);          */
+/*   NVAMD_GEMM_Y_TILED -- y is tiled [16 * ceil(m/16), n] (y_stride unused;  */
+/*   rows past m are neither read as inputs nor written).                     */
 /* Prologue: with x_ssq == NULL, a = x.  Otherwise x is the residual stream,  */
 /*   x_ssq[r * (k/32) + t] holds the sum of squares of x[r, 32t..32t+31], and */
 /*   a = bf16((x * rsqrt(sum_t x_ssq / k + eps)) * norm_weight); k <= 4096.  */
@@ -252,29 +263,33 @@ int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
 /* epilogue 2 (residual): y is the residual stream, updated in place:         */
 /*   y[r, c] = bf16(y[r, c] + bf16(acc)); y_ssq[r * (n/32) + t] = sum of      */
 /*   squares of the new y[r, 32t..32t+31] (the next prologue's x_ssq).        */
-/* n % 32 == 0, k % 256 == 0; x, w, x_ssq, norm_weight 16-byte aligned, y     */
-/* 8-byte aligned; row strides in elements (x, w: multiples of 8; y: of 4).   */
+/* n % 32 == 0, k % 256 == 0; x, w_tiled, x_ssq, norm_weight 16-byte aligned, */
+/* y 8-byte aligned; row strides in elements (x: multiple of 8; y: of 4).     */
 /* Shapes that split K over workgroups need a zero-filled workspace of        */
 /* nvamd_skinny_linear_workspace_size(n, k, epilogue) bytes (0: none); calls  */
 /* leave it zero-filled and must not overlap.  m > 32: NVAMD_EUNSUPPORTED.   */
 /* embed_rows: out[r] = table[ids[r]] (zeros for an id outside [0, vocab)),   */
 /*   the token embedding (torch.embedding at nv/layers/embed_head.py:20-21),  */
 /*   and, if ssq != NULL, ssq[r * (hidden/32) + t] = sum of squares of        */
-/*   out[r, 32t..32t+31].  hidden % 1024 == 0.                                */
+/*   out[r, 32t..32t+31].  hidden % 1024 == 0.  out_tiled != 0: out is tiled  */
+/*   (the layout above, out_stride unused).                                   */
 /* ------------------------------------------------------------------------- */
 size_t nvamd_skinny_linear_workspace_size(int n, int k, int epilogue);
 
+#define NVAMD_GEMM_X_TILED 1
+#define NVAMD_GEMM_Y_TILED 2
+
 int nvamd_skinny_linear(const void *x, int64_t x_stride, const float *x_ssq,
-                        const void *norm_weight, float eps, const void *w,
-                        int64_t w_stride, void *y, int64_t y_stride,
-                        float *y_ssq, int epilogue, int m, int n, int k,
-                        void *workspace, size_t workspace_bytes,
+                        const void *norm_weight, float eps,
+                        const void *w_tiled, void *y, int64_t y_stride,
+                        float *y_ssq, int epilogue, int flags, int m, int n,
+                        int k, void *workspace, size_t workspace_bytes,
                         hipStream_t stream);
 
 int nvamd_embed_rows(const int64_t *ids, const void *table,
                      int64_t table_stride, int vocab, void *out,
-                     int64_t out_stride, float *ssq, int rows, int hidden,
-                     hipStream_t stream);
+                     int64_t out_stride, int out_tiled, float *ssq, int rows,
+                     int hidden, hipStream_t stream);
 
 #ifdef __cplusplus
 }

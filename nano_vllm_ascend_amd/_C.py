@@ -65,10 +65,10 @@ _SIGNATURES = {
     "nvamd_skinny_linear_workspace_size": (_c_size, [_c_int, _c_int, _c_int]),
     "nvamd_skinny_linear": (
         _c_int,
-        [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_float, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_int, _c_int, _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_float, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_ptr, _c_size, _c_ptr]),
     "nvamd_embed_rows": (
-        _c_int, [_c_ptr, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_int, _c_int, _c_ptr]),
+        _c_int, [_c_ptr, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_int, _c_int, _c_ptr]),
     "nvamd_qk_norm_rope": (
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr,
@@ -421,23 +421,74 @@ def skinny_linear_workspace_size(n: int, k: int, epilogue: int = EPI_STORE) -> i
     return int(load().nvamd_skinny_linear_workspace_size(n, k, epilogue))
 
 
+GEMM_X_TILED = 1
+GEMM_Y_TILED = 2
+
+
+def is_tiled(t: torch.Tensor) -> bool:
+    """A tiled matrix is a contiguous [rows/16, cols/32, 512] tensor (the skinny GEMM's operand order)."""
+    return t.dim() == 3 and t.shape[2] == 512
+
+
+def tile(a: torch.Tensor) -> torch.Tensor:
+    """Row-major [R, C] (C % 32 == 0) -> tiled [ceil(R/16), C/32, 512]: 16 x 32 tiles, row-tile major,
+    element (r, c) of a tile at 128 * (c // 8) + 8 * r + c % 8.  Padding rows are zero."""
+    _require(a.dim() == 2 and a.shape[1] % 32 == 0, "tile() takes [R, C] with C % 32 == 0")
+    r, c = a.shape
+    rp = -(-r // 16) * 16
+    if rp != r:
+        a = torch.cat([a, a.new_zeros(rp - r, c)])
+    return a.reshape(rp // 16, 16, c // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(rp // 16, c // 32, 512).contiguous()
+
+
+def untile(t: torch.Tensor, rows: int | None = None) -> torch.Tensor:
+    """Tiled [R/16, C/32, 512] -> row-major [rows, C] (a copy; rows defaults to R)."""
+    _require(is_tiled(t), "untile() takes a tiled [R/16, C/32, 512] tensor")
+    rt, ct, _ = t.shape
+    a = t.reshape(rt, ct, 4, 16, 8).permute(0, 3, 1, 2, 4).reshape(rt * 16, ct * 32)
+    return (a if rows is None else a[:rows]).contiguous()
+
+
+def tiled_empty(rows: int, cols: int, device, dtype=torch.bfloat16) -> torch.Tensor:
+    """Uninitialised tiled storage for a [rows, cols] matrix (rows padded to a multiple of 16)."""
+    return torch.empty((-(-rows // 16), cols // 32, 512), dtype=dtype, device=device)
+
+
 def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, *, epilogue: int = EPI_STORE,
                   x_ssq: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
-                  y_ssq: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """Decode-batch projection x[M, K] @ w^T (M <= 32) with an optional RMSNorm prologue and a store,
-    SiLU*mul or residual-add epilogue (one HIP launch).  Returns the output (the residual for EPI_RESID)."""
+                  y_ssq: torch.Tensor | None = None, workspace: torch.Tensor | None = None, m: int | None = None,
+                  y_tiled: bool = False) -> torch.Tensor:
+    """Decode-batch projection x[M, K] @ W^T (M <= 32) with an optional RMSNorm prologue and a store,
+    SiLU*mul or residual-add epilogue (one HIP launch).  Returns the output (the residual for EPI_RESID).
+
+    w is the weight tiled (``tile(W)``; SILU: the fused [2I, K] gate/up weight).  x is row-major
+    [M, K] or tiled (then ``m`` gives the valid rows); with ``y_tiled`` the output (the residual
+    for EPI_RESID) is tiled with 16 * ceil(M/16) rows."""
     lib = load()
     _bf16_cuda("x", x)
     _bf16_cuda("w", w)
-    m, k = x.shape
-    _require(w.shape[1] == k, "w must be [N, K]")
-    n = w.shape[0] // 2 if epilogue == EPI_SILU else w.shape[0]
+    _require(is_tiled(w), "w must be tiled: tile(W)")
+    x_tiled = is_tiled(x)
+    if x_tiled:
+        _require(m is not None and 0 <= m <= 16 * x.shape[0], "a tiled x needs m <= its padded rows")
+        _require(m <= 16 or x.shape[0] >= 2, "a tiled x of more than 16 rows holds 32")
+        k = 32 * x.shape[1]
+    else:
+        m, k = x.shape
+    _require(32 * w.shape[1] == k, "w must be tiled [N/16, K/32, 512]")
+    n = 8 * w.shape[0] if epilogue == EPI_SILU else 16 * w.shape[0]
     if epilogue == EPI_RESID:
         _require(out is not None, "the residual epilogue updates `out` in place")
         _require(y_ssq is not None and y_ssq.dtype == torch.float32 and y_ssq.is_contiguous()
                  and y_ssq.numel() >= m * (n // 32), "y_ssq must be fp32 [M, N/32]")
-    out = torch.empty((m, n), dtype=x.dtype, device=x.device) if out is None else out
-    _require(out.shape == (m, n) and out.dtype == torch.bfloat16 and out.stride(1) == 1, "out must be bf16 [M, N]")
+    if y_tiled:
+        out = tiled_empty(max(m, 1), n, x.device) if out is None else out
+        _require(is_tiled(out) and out.dtype == torch.bfloat16 and out.shape[1] * 32 == n
+                 and 16 * out.shape[0] >= m and (m <= 16 or out.shape[0] >= 2), "out must be tiled bf16 [M, N]")
+    else:
+        out = torch.empty((m, n), dtype=x.dtype, device=x.device) if out is None else out
+        _require(out.shape == (m, n) and out.dtype == torch.bfloat16 and out.stride(1) == 1,
+                 "out must be bf16 [M, N]")
     if x_ssq is not None:
         _require(norm_weight is not None and norm_weight.dtype == torch.bfloat16 and norm_weight.numel() == k,
                  "norm_weight must be bf16 [K]")
@@ -446,41 +497,50 @@ def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = N
     need = skinny_linear_workspace_size(n, k, epilogue) if n % 32 == 0 and k % 256 == 0 else 0
     if need and workspace is None:
         workspace = torch.zeros(need, dtype=torch.uint8, device=x.device)
+    flags = (GEMM_X_TILED if x_tiled else 0) | (GEMM_Y_TILED if y_tiled else 0)
     status = lib.nvamd_skinny_linear(
-        x.data_ptr(), _row_stride(x), _ptr(x_ssq), _ptr(norm_weight), float(eps), w.data_ptr(), _row_stride(w),
-        out.data_ptr(), out.stride(0), _ptr(y_ssq), int(epilogue), m, n, k, _ptr(workspace),
-        workspace.numel() if workspace is not None else 0, _stream())
+        x.data_ptr(), 0 if x_tiled else _row_stride(x), _ptr(x_ssq), _ptr(norm_weight), float(eps), w.data_ptr(),
+        out.data_ptr(), 0 if y_tiled else out.stride(0), _ptr(y_ssq), int(epilogue), flags, m, n, k,
+        _ptr(workspace), workspace.numel() if workspace is not None else 0, _stream())
     _check(status, "nvamd_skinny_linear")
     return out
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
+def linear(x: torch.Tensor, w_tiled: torch.Tensor, out: torch.Tensor | None = None,
            workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """x[M, K] @ w[N, K]^T in bf16 for M <= 32 (HIP skinny GEMM)."""
-    return skinny_linear(x, w, out, workspace=workspace)
+    """x[M, K] @ W[N, K]^T in bf16 for M <= 32 (HIP skinny GEMM; w_tiled = tile(W))."""
+    return skinny_linear(x, w_tiled, out, workspace=workspace)
 
 
-def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor, out: torch.Tensor | None = None,
+def linear_silu_mul(x: torch.Tensor, w_gate_up_tiled: torch.Tensor, out: torch.Tensor | None = None,
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """silu(x @ w_gate_up[:I]^T) * (x @ w_gate_up[I:]^T) in bf16 for M <= 32 (one HIP launch)."""
-    _require(w_gate_up.shape[0] % 2 == 0, "w_gate_up must be [2I, K]")
-    return skinny_linear(x, w_gate_up, out, epilogue=EPI_SILU, workspace=workspace)
+    """silu(x @ W[:I]^T) * (x @ W[I:]^T) in bf16 for M <= 32 (one HIP launch; W the [2I, K] gate/up
+    weight, passed as tile(W))."""
+    _require(w_gate_up_tiled.shape[0] % 2 == 0, "the gate/up weight must be [2I, K]")
+    return skinny_linear(x, w_gate_up_tiled, out, epilogue=EPI_SILU, workspace=workspace)
 
 
 def embed_rows(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None = None,
-               ssq: torch.Tensor | None = None) -> torch.Tensor:
-    """table[ids] (zero rows for ids outside the vocab) and, if given, per-32-column sums of squares."""
+               ssq: torch.Tensor | None = None, out_tiled: bool = False) -> torch.Tensor:
+    """table[ids] (zero rows for ids outside the vocab) and, if given, per-32-column sums of squares.
+    With ``out_tiled`` the rows are written tiled (16 * ceil(rows/16) padded rows, padding untouched)."""
     lib = load()
     _bf16_cuda("table", table)
     _require(ids.dtype == torch.int64 and ids.is_cuda and ids.is_contiguous(), "ids must be int64 on the GPU")
     rows = ids.numel()
     vocab, hidden = table.shape
-    out = torch.empty((rows, hidden), dtype=table.dtype, device=table.device) if out is None else out
-    _require(out.shape == (rows, hidden) and out.dtype == torch.bfloat16, "out must be bf16 [rows, hidden]")
+    if out_tiled:
+        out = tiled_empty(max(rows, 1), hidden, table.device) if out is None else out
+        _require(is_tiled(out) and out.dtype == torch.bfloat16 and out.shape[1] * 32 == hidden
+                 and 16 * out.shape[0] >= rows, "out must be tiled bf16 [rows, hidden]")
+    else:
+        out = torch.empty((rows, hidden), dtype=table.dtype, device=table.device) if out is None else out
+        _require(out.shape == (rows, hidden) and out.dtype == torch.bfloat16, "out must be bf16 [rows, hidden]")
     if ssq is not None:
         _require(ssq.dtype == torch.float32 and ssq.is_contiguous() and ssq.numel() >= rows * (hidden // 32),
                  "ssq must be fp32 [rows, hidden/32]")
     status = lib.nvamd_embed_rows(ids.data_ptr(), table.data_ptr(), _row_stride(table), vocab, out.data_ptr(),
-                                  _row_stride(out), _ptr(ssq), rows, hidden, _stream())
+                                  0 if out_tiled else _row_stride(out), int(out_tiled), _ptr(ssq), rows, hidden,
+                                  _stream())
     _check(status, "nvamd_embed_rows")
     return out

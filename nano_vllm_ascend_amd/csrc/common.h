@@ -182,6 +182,13 @@ __device__ __forceinline__ void st16(u16 *p, u32x4 v) { *reinterpret_cast<u32x4 
 
 __host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Element (r, c) of a tiled [rows, cols] bf16 matrix (the skinny GEMM's operand order): 16 x 32
+// tiles of 512 elements, row-tile major; inside a tile, 128 * (c%32 / 8) + 8 * (r%16) + c%8, so
+// MFMA lane (r%16) + 16 * (c%32 / 8) finds its 8 consecutive columns at 8 * lane.
+__device__ __forceinline__ int64_t tiled_index(int r, int c, int cols) {
+  return ((int64_t)(r >> 4) * (cols >> 5) + (c >> 5)) * 512 + ((c & 31) >> 3) * 128 + (r & 15) * 8 + (c & 7);
+}
+
 inline int log2_exact(int x) {
   if (x <= 0 || (x & (x - 1)) != 0) return -1;
   int l = 0;

@@ -157,10 +157,12 @@ argmax_rows_kernel(const u16 *__restrict__ logits, int64_t row_stride, int vocab
 
 // One wave per row: out[r] = table[ids[r]] (a zero row for an id outside [0, vocab)),
 // and ssq[r][t] = sum of squares of columns 32t..32t+31.  Lane l holds columns
-// 16l..16l+15 of each 1024-wide chunk; lanes 2t and 2t+1 make up tile t.
+// 16l..16l+15 of each 1024-wide chunk; lanes 2t and 2t+1 make up tile t.  A tiled out
+// (the skinny GEMM's operand order) takes each 8-column half as one 16-byte store.
 __global__ void __launch_bounds__(256)
 embed_rows_kernel(const int64_t *__restrict__ ids, const u16 *__restrict__ table, int64_t table_stride, int vocab,
-                  u16 *__restrict__ out, int64_t out_stride, float *__restrict__ ssq, int rows, int hidden) {
+                  u16 *__restrict__ out, int64_t out_stride, bool out_tiled, float *__restrict__ ssq, int rows,
+                  int hidden) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
@@ -173,8 +175,13 @@ embed_rows_kernel(const int64_t *__restrict__ ids, const u16 *__restrict__ table
     const int off = ch + 16 * lane;
     const u32x4 a = valid ? ld16(src + off) : z;
     const u32x4 b = valid ? ld16(src + off + 8) : z;
-    st16(dst + off, a);
-    st16(dst + off + 8, b);
+    if (out_tiled) {
+      st16(out + tiled_index(row, off, hidden), a);
+      st16(out + tiled_index(row, off + 8, hidden), b);
+    } else {
+      st16(dst + off, a);
+      st16(dst + off + 8, b);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -235,15 +242,16 @@ extern "C" int nvamd_argmax_rows(const void *logits, int64_t row_stride, int row
 }
 
 extern "C" int nvamd_embed_rows(const int64_t *ids, const void *table, int64_t table_stride, int vocab, void *out,
-                                int64_t out_stride, float *ssq, int rows, int hidden, hipStream_t stream) {
+                                int64_t out_stride, int out_tiled, float *ssq, int rows, int hidden,
+                                hipStream_t stream) {
   if (rows == 0) return NVAMD_OK;
   if (!ids || !table || !out || rows < 0 || vocab <= 0) return NVAMD_EINVAL;
   if (hidden <= 0 || hidden % 1024) return NVAMD_EUNSUPPORTED;
-  if (!aligned16(table) || !aligned16(out) || table_stride < hidden || table_stride % 8 || out_stride < hidden ||
-      out_stride % 8)
+  if (!aligned16(table) || !aligned16(out) || table_stride < hidden || table_stride % 8 ||
+      (!out_tiled && (out_stride < hidden || out_stride % 8)))
     return NVAMD_EINVAL;
   hipLaunchKernelGGL(embed_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, ids,
-                     static_cast<const u16 *>(table), table_stride, vocab, static_cast<u16 *>(out), out_stride, ssq,
-                     rows, hidden);
+                     static_cast<const u16 *>(table), table_stride, vocab, static_cast<u16 *>(out), out_stride,
+                     out_tiled != 0, ssq, rows, hidden);
   return launch_status();
 }

@@ -7,10 +7,14 @@
 // At M <= 32 a projection is a weight stream (2 B of W per 2*M FLOP), so the kernel is
 // shaped to keep every W byte in flight at once, read it once, and keep the per-CU
 // address path at full rate:
-//   * v_mfma_f32_16x16x32_bf16 with A = 16 batch rows of X (one or two M tiles; rows
-//     past M repeat row M-1 and are dropped) and B = 16 rows of W.  Lane (n, g) feeds
-//     column n with k = 8g..8g+7 of each 32-wide step, so one load instruction covers
-//     16 rows x 64 contiguous bytes: 16 whole 64-byte segments per KB of data;
+//   * v_mfma_f32_16x16x32_bf16 with A = 16 batch rows of X (one or two M tiles) and
+//     B = 16 rows of W.  Lane (n, g) feeds row n with k = 8g..8g+7 of each 32-wide step.
+//     W, and X and Y where the caller asks for it, are stored in that fragment order
+//     ("tiled": 16 x 32 tiles of 512 elements, lane l's 8 elements at 8l), so one load
+//     instruction reads 1 KB of contiguous memory.  Against row-major operands (16 rows x
+//     64 bytes per instruction) this halves the vector L1 accesses that bound the
+//     M = 32 projections (qkv 6.4 -> 4.9 us).  Row-major X rows past M repeat row M-1;
+//     a tiled X holds 16 * ceil(M/16) rows, and rows past M only reach dropped outputs;
 //   * a workgroup of NW waves owns 16*NT output columns and one of KS slices of K
 //     (split-K across workgroups where the column count alone gives too few
 //     workgroups); its waves split the slice again, and a wave's NT column tiles share
@@ -42,14 +46,15 @@ constexpr int kSsqVec = kMaxNormK / 128 / 4;  // 16-byte partial-sum loads per l
 
 struct GemmArgs {
   const u16 *x;
-  int64_t x_stride;
+  int64_t x_stride;         // row-major X; a tiled X has none
   const float *x_ssq;       // NORM: [m][k / 32]
   const u16 *norm_w;        // NORM: [k]
   float eps;
-  const u16 *w;
-  int64_t w_stride;
+  const u16 *w;             // tiled [n (SILU: 2n), k]
   u16 *y;                   // STORE / SILU output; RESID: the residual, updated in place
-  int64_t y_stride;
+  int64_t y_stride;         // row-major Y
+  bool x_tiled;
+  bool y_tiled;
   float *y_ssq;             // RESID: [m][n / 32]
   int m;
   int n;                    // output columns (SILU: inter)
@@ -61,6 +66,7 @@ struct GemmArgs {
 };
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
 
 __device__ __forceinline__ void store_agent4(float *p, f32x4 v) {
   const uint64_t lo = (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32);
@@ -105,18 +111,21 @@ skinny_gemm_kernel(GemmArgs a) {
   const int slice = blockIdx.x - group * a.ks;
   const int n0 = group * CW;
 
+  // Operand addresses: base + k0 * step for the 32-wide K step starting at k0 (tiled: the
+  // step's 512-element tile follows the previous one, so 16 elements per unit of k).
   int xr[MT];
   const u16 *xp[MT];
+  const int xs = a.x_tiled ? 16 : 1;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     xr[mt] = min(16 * mt + n, a.m - 1);
-    xp[mt] = a.x + (int64_t)xr[mt] * a.x_stride + 8 * g;
+    xp[mt] = a.x_tiled ? a.x + (int64_t)mt * (a.k >> 5) * 512 + 8 * lane : a.x + (int64_t)xr[mt] * a.x_stride + 8 * g;
   }
   const u16 *wp[NACC];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    wp[t] = a.w + (int64_t)(n0 + 16 * t + n) * a.w_stride + 8 * g;
-    if (EPI == kEpiSilu) wp[NT + t] = wp[t] + (int64_t)a.n * a.w_stride;
+    wp[t] = a.w + (int64_t)(group * NT + t) * (a.k >> 5) * 512 + 8 * lane;
+    if (EPI == kEpiSilu) wp[NT + t] = wp[t] + (int64_t)(a.n >> 4) * (a.k >> 5) * 512;
   }
   const u16 *np = NORM ? a.norm_w + 8 * g : nullptr;
 
@@ -152,9 +161,9 @@ skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int b = 0; b < KB; ++b) {
 #pragma unroll
-      for (int t = 0; t < NACC; ++t) wv[b][t] = ld16(wp[t] + k0 + 32 * b);
+      for (int t = 0; t < NACC; ++t) wv[b][t] = ld16(wp[t] + (int64_t)(k0 + 32 * b) * 16);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xv[b][mt] = ld16(xp[mt] + k0 + 32 * b);
+      for (int mt = 0; mt < MT; ++mt) xv[b][mt] = ld16(xp[mt] + (int64_t)(k0 + 32 * b) * xs);
       if (NORM) nv[b] = ld16(np + k0 + 32 * b);
     }
     // every load of the round is issued before the first MFMA waits on one
@@ -250,7 +259,7 @@ skinny_gemm_kernel(GemmArgs a) {
       }
     }
     const int c = n0 + cl;
-    u16 *yp = a.y + (int64_t)row * a.y_stride + c;
+    u16 *yp = a.y + (a.y_tiled ? tiled_index(row, c, a.n) : (int64_t)row * a.y_stride + c);
     if (EPI == kEpiStore) {
       if (row < a.m)
         *reinterpret_cast<u32x2 *>(yp) = u32x2{pack_bf16x2(v[0][0], v[0][1]), pack_bf16x2(v[0][2], v[0][3])};
@@ -261,7 +270,8 @@ skinny_gemm_kernel(GemmArgs a) {
       if (row < a.m) *reinterpret_cast<u32x2 *>(yp) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     } else {  // RESID
       const int rr = min(row, a.m - 1);
-      const u32x2 r = *reinterpret_cast<const u32x2 *>(a.y + (int64_t)rr * a.y_stride + c);
+      const u32x2 r = *reinterpret_cast<const u32x2 *>(
+          a.y + (a.y_tiled ? tiled_index(rr, c, a.n) : (int64_t)rr * a.y_stride + c));
       const u32 h0 = pack_bf16x2(bf16_lo(r[0]) + round_bf16(v[0][0]), bf16_hi(r[0]) + round_bf16(v[0][1]));
       const u32 h1 = pack_bf16x2(bf16_lo(r[1]) + round_bf16(v[0][2]), bf16_hi(r[1]) + round_bf16(v[0][3]));
       float ss = bf16_lo(h0) * bf16_lo(h0) + bf16_hi(h0) * bf16_hi(h0) + bf16_lo(h1) * bf16_lo(h1) +
@@ -351,18 +361,21 @@ extern "C" size_t nvamd_skinny_linear_workspace_size(int n, int k, int epilogue)
 }
 
 extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float *x_ssq, const void *norm_weight,
-                                   float eps, const void *w, int64_t w_stride, void *y, int64_t y_stride,
-                                   float *y_ssq, int epilogue, int m, int n, int k, void *workspace,
+                                   float eps, const void *w_tiled, void *y, int64_t y_stride, float *y_ssq,
+                                   int epilogue, int flags, int m, int n, int k, void *workspace,
                                    size_t workspace_bytes, hipStream_t stream) {
   if (m == 0) return NVAMD_OK;
-  if (!x || !w || !y || m < 0 || n <= 0 || k <= 0 || epilogue < 0 || epilogue > 2) return NVAMD_EINVAL;
+  if (!x || !w_tiled || !y || m < 0 || n <= 0 || k <= 0 || epilogue < 0 || epilogue > 2 ||
+      (flags & ~(NVAMD_GEMM_X_TILED | NVAMD_GEMM_Y_TILED)))
+    return NVAMD_EINVAL;
   if (m > 32 || n % 32 != 0 || k % 256 != 0) return NVAMD_EUNSUPPORTED;
+  const bool x_tiled = flags & NVAMD_GEMM_X_TILED, y_tiled = flags & NVAMD_GEMM_Y_TILED;
   const bool norm = x_ssq != nullptr;
   if (norm && !norm_weight) return NVAMD_EINVAL;
   if (norm && k > kMaxNormK) return NVAMD_EUNSUPPORTED;
   if (epilogue == kEpiResid && !y_ssq) return NVAMD_EINVAL;
-  if (!aligned16(x) || !aligned16(w) || x_stride % 8 || w_stride % 8 || x_stride < k || w_stride < k ||
-      y_stride < n || (reinterpret_cast<uintptr_t>(y) & 7u) || y_stride % 4 ||
+  if (!aligned16(x) || !aligned16(w_tiled) || (reinterpret_cast<uintptr_t>(y) & 7u) ||
+      (!x_tiled && (x_stride % 8 || x_stride < k)) || (!y_tiled && (y_stride < n || y_stride % 4)) ||
       (norm && (!aligned16(x_ssq) || !aligned16(norm_weight))))
     return NVAMD_EINVAL;
   const Plan p = make_plan(n, k, epilogue);
@@ -379,10 +392,11 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
   a.x_ssq = x_ssq;
   a.norm_w = static_cast<const u16 *>(norm_weight);
   a.eps = eps;
-  a.w = static_cast<const u16 *>(w);
-  a.w_stride = w_stride;
+  a.w = static_cast<const u16 *>(w_tiled);
   a.y = static_cast<u16 *>(y);
   a.y_stride = y_stride;
+  a.x_tiled = x_tiled;
+  a.y_tiled = y_tiled;
   a.y_ssq = y_ssq;
   a.m = m;
   a.n = n;

@@ -200,25 +200,27 @@ class Sampler:
         return out
 
 
-def _skinny_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
-    return (x.is_cuda and x.dim() == 2 and 0 < x.shape[0] <= _C.SKINNY_MAX_ROWS and x.dtype == torch.bfloat16
-            and weight.dtype == torch.bfloat16 and x.stride(1) == 1 and weight.is_contiguous()
+def _skinny_ok(x: torch.Tensor, weight: torch.Tensor, tiled: torch.Tensor | None) -> bool:
+    return (tiled is not None and x.is_cuda and x.dim() == 2 and 0 < x.shape[0] <= _C.SKINNY_MAX_ROWS
+            and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.stride(1) == 1
             and weight.shape[0] % 32 == 0 and x.shape[1] % 256 == 0 and x.data_ptr() % 16 == 0
             and x.stride(0) % 8 == 0)
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, skinny: bool = True) -> torch.Tensor:
-    """x @ weight^T.  Decode batches (<= 32 rows) use the skinny-M HIP kernel, which streams
-    the weight once; larger batches (prefill) use the library GEMM.  ``skinny=False`` keeps a
-    projection on the library GEMM where that measures faster (N = 1024 outputs)."""
-    if skinny and _skinny_ok(x, weight):
-        return _C.linear(x, weight)
+def linear(x: torch.Tensor, weight: torch.Tensor, skinny: bool = True,
+           tiled: torch.Tensor | None = None) -> torch.Tensor:
+    """x @ weight^T.  Batches of <= 32 rows use the skinny-M HIP kernel when the weight's tiled
+    copy (``_C.tile(weight)``) is given -- it streams the weight once; otherwise, and for larger
+    batches (prefill), the library GEMM.  ``skinny=False`` keeps a projection on the library GEMM."""
+    if skinny and _skinny_ok(x, weight, tiled):
+        return _C.linear(x, tiled)
     return F.linear(x, weight)
 
 
-def gate_up_silu(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+def gate_up_silu(x: torch.Tensor, w_gate_up: torch.Tensor, tiled: torch.Tensor | None = None) -> torch.Tensor:
     """silu(x @ W_gate^T) * (x @ W_up^T) for the fused [2I, H] weight (nv/models/qwen3.py:34-35):
-    one HIP launch for decode batches, library GEMM + silu_mul kernel otherwise."""
-    if _skinny_ok(x, w_gate_up) and (w_gate_up.shape[0] // 2) % 32 == 0:
-        return _C.linear_silu_mul(x, w_gate_up)
+    one HIP launch for batches of <= 32 rows when the weight's tiled copy is given, library GEMM +
+    silu_mul kernel otherwise."""
+    if _skinny_ok(x, w_gate_up, tiled) and (w_gate_up.shape[0] // 2) % 32 == 0:
+        return _C.linear_silu_mul(x, tiled)
     return _C.silu_mul(F.linear(x, w_gate_up))

@@ -13,7 +13,11 @@ skinny-M HIP GEMM runs every projection, each RMSNorm in the prologue of the GEM
 that consumes it, and each residual add in the epilogue of the GEMM that produces
 it (with the per-32-column sums of squares the next norm needs), and SiLU*mul in
 the gate/up epilogue -- 5 launches per layer instead of 9, same rounding points.
-Prefill and larger batches run the unfused chain on hipBLASLt + add_rms_norm.
+That path reads tiled copies of the projection weights (the GEMM's operand order,
+built once by ``build_decode_weights``) and keeps the residual stream and the SiLU
+output tiled as well; the qkv output, the attention output and the logits stay
+row-major.  Prefill and larger batches run the unfused chain on hipBLASLt +
+add_rms_norm over the row-major weights.
 """
 from __future__ import annotations
 
@@ -51,10 +55,16 @@ class Qwen3Attention(nn.Module):
         self.prefill_attn = HipBatchPrefillAttention(self.num_heads, self.num_kv_heads, self.head_dim, block_size,
                                                      max_model_len)
         self.paged_attn = HipPagedAttention(self.num_heads, self.num_kv_heads, self.head_dim)
+        self.qkv_tiled = None  # tiled copies for the fused decode path (build_tiled)
+        self.o_tiled = None
+
+    def build_tiled(self) -> None:
+        self.qkv_tiled = _C.tile(self.qkv_weight.detach())
+        self.o_tiled = _C.tile(self.o_weight.detach())
 
     def forward(self, hidden_states, rotary: RotaryEmbedding, positions, kv_cache, attn_metadata, is_prefill: bool):
         t = hidden_states.shape[0]
-        qkv = linear(hidden_states, self.qkv_weight)
+        qkv = linear(hidden_states, self.qkv_weight, tiled=self.qkv_tiled)
         q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
@@ -76,19 +86,19 @@ class Qwen3Attention(nn.Module):
                                            max_context_len=getattr(attn_metadata, "max_context_bound", None),
                                            workspace=getattr(attn_metadata, "decode_workspace", None))
 
-    def decode_fused(self, residual, ssq, norm: RMSNorm, rotary, positions, kv_cache, attn_metadata, workspace):
+    def decode_fused(self, residual, ssq, t: int, norm: RMSNorm, rotary, positions, kv_cache, attn_metadata,
+                     workspace):
         """residual += o_proj(attention(qkv_proj(norm(residual)))) in place, for a decode batch of
-        <= 32 rows: the input RMSNorm runs in the qkv GEMM's prologue and the residual add (with
-        the sums of squares the next norm needs) in the o_proj GEMM's epilogue."""
-        t = residual.shape[0]
-        qkv = _C.skinny_linear(residual, self.qkv_weight, x_ssq=ssq, norm_weight=norm.weight,
-                               eps=norm.variance_epsilon, workspace=workspace)
+        t <= 32 rows held tiled in `residual`: the input RMSNorm runs in the qkv GEMM's prologue and
+        the residual add (with the sums of squares the next norm needs) in the o_proj GEMM's epilogue."""
+        qkv = _C.skinny_linear(residual, self.qkv_tiled, x_ssq=ssq, norm_weight=norm.weight,
+                               eps=norm.variance_epsilon, workspace=workspace, m=t)
         q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
         attn = self.decode_attention(q, k, v, rotary, positions, kv_cache, attn_metadata)
-        _C.skinny_linear(attn.reshape(t, self.q_size), self.o_weight, residual, epilogue=_C.EPI_RESID, y_ssq=ssq,
-                         workspace=workspace)
+        _C.skinny_linear(attn.reshape(t, self.q_size), self.o_tiled, residual, epilogue=_C.EPI_RESID, y_ssq=ssq,
+                         workspace=workspace, y_tiled=True)
 
 
 class Qwen3MLP(nn.Module):
@@ -97,17 +107,25 @@ class Qwen3MLP(nn.Module):
         self.intermediate = config.intermediate_size
         self.gate_up_weight = nn.Parameter(torch.empty(2 * config.intermediate_size, config.hidden_size))
         self.down_weight = nn.Parameter(torch.empty(config.hidden_size, config.intermediate_size))
+        self.gate_up_tiled = None  # tiled copies for the fused decode path (build_tiled)
+        self.down_tiled = None
+
+    def build_tiled(self) -> None:
+        self.gate_up_tiled = _C.tile(self.gate_up_weight.detach())
+        self.down_tiled = _C.tile(self.down_weight.detach())
 
     def forward(self, x):
-        return linear(gate_up_silu(x, self.gate_up_weight), self.down_weight, skinny=False)
+        return linear(gate_up_silu(x, self.gate_up_weight, self.gate_up_tiled), self.down_weight, skinny=False)
 
-    def decode_fused(self, residual, ssq, norm: RMSNorm, workspace):
-        """residual += down(silu(gate(norm(residual))) * up(norm(residual))) in place (<= 32 rows):
-        norm in the gate/up GEMM's prologue, SiLU*mul in its epilogue, the residual add in the
-        down GEMM's epilogue."""
-        act = _C.skinny_linear(residual, self.gate_up_weight, epilogue=_C.EPI_SILU, x_ssq=ssq,
-                               norm_weight=norm.weight, eps=norm.variance_epsilon, workspace=workspace)
-        _C.skinny_linear(act, self.down_weight, residual, epilogue=_C.EPI_RESID, y_ssq=ssq, workspace=workspace)
+    def decode_fused(self, residual, ssq, t: int, norm: RMSNorm, workspace):
+        """residual += down(silu(gate(norm(residual))) * up(norm(residual))) in place (t <= 32 rows,
+        tiled): norm in the gate/up GEMM's prologue, SiLU*mul in its epilogue (written tiled), the
+        residual add in the down GEMM's epilogue."""
+        act = _C.skinny_linear(residual, self.gate_up_tiled, epilogue=_C.EPI_SILU, x_ssq=ssq,
+                               norm_weight=norm.weight, eps=norm.variance_epsilon, workspace=workspace, m=t,
+                               y_tiled=True)
+        _C.skinny_linear(act, self.down_tiled, residual, epilogue=_C.EPI_RESID, y_ssq=ssq, workspace=workspace, m=t,
+                         y_tiled=True)
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -149,16 +167,16 @@ class Qwen3Model(nn.Module):
     def forward_decode_fused(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, workspace):
         """Decode forward for <= 32 rows with every RMSNorm and residual add folded into the
         projections: 5 launches per layer (qkv, norm/RoPE/store + attention, o, gate_up, down).
-        Returns the final residual stream and its per-32-column sums of squares; the final
-        norm runs in the LM head's prologue."""
+        Returns the final residual stream (tiled, 16 * ceil(t/16) rows) and its per-32-column sums
+        of squares; the final norm runs in the LM head's prologue."""
         t = input_ids_flat.shape[0]
         hidden = self.embed_tokens.shape[1]
         ssq = torch.empty((t, hidden // 32), dtype=torch.float32, device=self.embed_tokens.device)
-        residual = _C.embed_rows(input_ids_flat, self.embed_tokens, ssq=ssq)
+        residual = _C.embed_rows(input_ids_flat, self.embed_tokens, ssq=ssq, out_tiled=True)
         for layer in self.layers:
-            layer.self_attn.decode_fused(residual, ssq, layer.input_layernorm, self.rotary_emb, position_ids_flat,
+            layer.self_attn.decode_fused(residual, ssq, t, layer.input_layernorm, self.rotary_emb, position_ids_flat,
                                          kv_cache, attn_metadata, workspace)
-            layer.mlp.decode_fused(residual, ssq, layer.post_attention_layernorm, workspace)
+            layer.mlp.decode_fused(residual, ssq, t, layer.post_attention_layernorm, workspace)
         return residual, ssq
 
 
@@ -171,6 +189,28 @@ class Qwen3ForCausalLM(nn.Module):
             torch.empty(config.vocab_size, config.hidden_size))
 
         self._gemm_workspace = None
+        self.lm_head_tiled = None
+        self._tiled_ready = False
+
+    def build_decode_weights(self) -> None:
+        """Tiled copies of the projection and LM head weights for the fused decode path (about the
+        size of the weights again).  Built on the first fused decode; call it again after changing
+        weights in place."""
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the tiled decode weights must be built before graph capture")
+        for layer in self.model.layers:
+            layer.self_attn.build_tiled()
+            layer.mlp.build_tiled()
+        self.lm_head_tiled = _C.tile(self.lm_head.detach())
+        self._tiled_ready = True
+
+    def _drop_decode_weights(self) -> None:
+        """Forget the tiled copies (the weights are about to change)."""
+        for layer in self.model.layers:
+            layer.self_attn.qkv_tiled = layer.self_attn.o_tiled = None
+            layer.mlp.gate_up_tiled = layer.mlp.down_tiled = None
+        self.lm_head_tiled = None
+        self._tiled_ready = False
 
     def decode_fusable(self, rows: int) -> bool:
         """Whether a decode batch of `rows` runs on the fused skinny-GEMM path."""
@@ -194,22 +234,26 @@ class Qwen3ForCausalLM(nn.Module):
     def forward(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill: bool,
                 logits_indices=None) -> CausalLMOutput:
         if not is_prefill and logits_indices is None and self.decode_fusable(input_ids_flat.shape[0]):
+            if not self._tiled_ready:
+                self.build_decode_weights()
             ws = self.gemm_workspace()
             residual, ssq = self.model.forward_decode_fused(input_ids_flat, position_ids_flat, kv_cache,
                                                             attn_metadata, ws)
             norm = self.model.norm
-            return CausalLMOutput(logits=_C.skinny_linear(residual, self.lm_head, x_ssq=ssq, norm_weight=norm.weight,
-                                                          eps=norm.variance_epsilon, workspace=ws))
+            return CausalLMOutput(logits=_C.skinny_linear(residual, self.lm_head_tiled, x_ssq=ssq,
+                                                          norm_weight=norm.weight, eps=norm.variance_epsilon,
+                                                          workspace=ws, m=input_ids_flat.shape[0]))
         h = self.model(input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill)
         if logits_indices is not None:
             h = h.index_select(0, logits_indices)
-        return CausalLMOutput(logits=linear(h, self.lm_head))
+        return CausalLMOutput(logits=linear(h, self.lm_head, tiled=self.lm_head_tiled))
 
     # ---------------------------------------------------------------- weights
     @torch.no_grad()
     def init_random(self, seed: int = 0, std: float | None = None) -> None:
         """Seeded N(0, std) for every projection and the embedding, ones for every norm weight."""
         std = self.config.initializer_range if std is None else std
+        self._drop_decode_weights()
         dev = self.model.embed_tokens.device
         gen = torch.Generator(device=dev)
         gen.manual_seed(seed)
@@ -225,6 +269,7 @@ class Qwen3ForCausalLM(nn.Module):
     def load_hf_state_dict(self, sd: dict) -> list[str]:
         """Copy HF Qwen3ForCausalLM weights (q/k/v and gate/up are concatenated); returns missing names."""
         missing = []
+        self._drop_decode_weights()
         m = self.model
 
         def put(dst, name):

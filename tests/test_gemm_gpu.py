@@ -2,7 +2,8 @@
 
 The kernel accumulates in fp32 and rounds to bf16 once, so each output is within one bf16 ulp of
 the fp32 product of the same bf16 operands: half an ulp is at most 2^-8 of the value, and the
-additive slack covers the fp32 summation-order difference.
+additive slack covers the fp32 summation-order difference.  Weights are passed tiled
+(``_C.tile``); tiled activations and outputs must give bit-identical results to row-major ones.
 """
 from __future__ import annotations
 
@@ -38,7 +39,7 @@ def _assert_close_bf16(y, ref, rel=ULP, slack=1e-5):
 def test_linear_matches_fp32(device, m, nk):
     n, k = nk
     x, w = _operands(m, n, k, device, seed=m * 7 + n)
-    y = _C.linear(x, w)
+    y = _C.linear(x, _C.tile(w))
     ref = x.float() @ w.float().t()
     torch.cuda.synchronize()
     _assert_close_bf16(y, ref)
@@ -62,7 +63,7 @@ def test_linear_silu_mul_matches_unfused_rounding(device, m):
     s' within one bf16 step of the fp32 reference's values."""
     inter, k = 3072, 1024
     x, w = _operands(m, 2 * inter, k, device, seed=100 + m)
-    y = _C.linear_silu_mul(x, w)
+    y = _C.linear_silu_mul(x, _C.tile(w))
     full = x.float() @ w.float().t()
     g = full[:, :inter].to(torch.bfloat16)
     u = full[:, inter:].to(torch.bfloat16)
@@ -81,7 +82,7 @@ def test_linear_silu_mul_matches_unfused_rounding(device, m):
                                  f"y={y[bad].tolist()} chain={chain[bad].tolist()} g={g[bad].tolist()} "
                                  f"u={u[bad].tolist()}")
     # and the fused launch agrees with the kernel's own unfused chain to the same rule
-    two = _C.silu_mul(_C.linear(x, w))
+    two = _C.silu_mul(_C.linear(x, _C.tile(w)))
     assert ((two.float() - y.float()).abs() <= 4 * ULP * y.float().abs() + 1e-3).float().mean().item() > 0.999
 
 
@@ -92,7 +93,7 @@ def test_linear_strided_input_and_output(device):
     xbuf = torch.zeros((m, k + 256), dtype=torch.bfloat16, device=device)
     xbuf[:, 128 : 128 + k] = x
     ybuf = torch.zeros((m, n + 64), dtype=torch.bfloat16, device=device)
-    y = _C.linear(xbuf[:, 128 : 128 + k], w, out=ybuf[:, 32 : 32 + n])
+    y = _C.linear(xbuf[:, 128 : 128 + k], _C.tile(w), out=ybuf[:, 32 : 32 + n])
     torch.cuda.synchronize()
     _assert_close_bf16(y, x.float() @ w.float().t())
     assert int(ybuf[:, :32].abs().sum()) == 0 and int(ybuf[:, 32 + n :].abs().sum()) == 0
@@ -101,8 +102,9 @@ def test_linear_strided_input_and_output(device):
 @pytest.mark.gpu
 def test_linear_is_deterministic(device):
     x, w = _operands(32, 4096, 1024, device, seed=8)
-    a = _C.linear(x, w)
-    b = _C.linear(x, w)
+    wt = _C.tile(w)
+    a = _C.linear(x, wt)
+    b = _C.linear(x, wt)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
 
@@ -110,6 +112,13 @@ def test_linear_is_deterministic(device):
 @pytest.mark.gpu
 def test_linear_rejects_more_than_32_rows(device):
     x, w = _operands(33, 1024, 1024, device, seed=9)
+    with pytest.raises(ValueError):
+        _C.linear(x, _C.tile(w))
+
+
+@pytest.mark.gpu
+def test_linear_rejects_a_row_major_weight(device):
+    x, w = _operands(4, 1024, 1024, device, seed=9)
     with pytest.raises(ValueError):
         _C.linear(x, w)
 
@@ -129,11 +138,12 @@ def test_norm_prologue_matches_add_rms_norm_then_linear(device, m, nk):
     gen = torch.Generator(device=device).manual_seed(5)
     nw = (1.0 + 0.02 * torch.randn(k, generator=gen, device=device)).to(torch.bfloat16)
     ssq = _tile_ssq(x).contiguous()
-    y = _C.skinny_linear(x, w, x_ssq=ssq, norm_weight=nw, eps=1e-6)
+    wt = _C.tile(w)
+    y = _C.skinny_linear(x, wt, x_ssq=ssq, norm_weight=nw, eps=1e-6)
     # the unfused chain: the standalone RMSNorm kernel, then the plain projection
     a = torch.empty_like(x)
     _C.add_rms_norm(None, x.clone(), nw, a, 1e-6)
-    y2 = _C.linear(a, w)
+    y2 = _C.linear(a, wt)
     # fp32 emulation of the prologue's rounding
     rstd = torch.rsqrt(ssq.sum(-1, keepdim=True) / k + 1e-6)
     a_ref = ((x.float() * rstd) * nw.float()).to(torch.bfloat16)
@@ -156,7 +166,7 @@ def test_residual_epilogue(device, m, k):
     r0 = torch.randn((m, n), generator=gen, device=device).to(torch.bfloat16)
     r = r0.clone()
     ssq = torch.full((m, n // 32), -1.0, device=device)
-    _C.skinny_linear(x, w, r, epilogue=_C.EPI_RESID, y_ssq=ssq)
+    _C.skinny_linear(x, _C.tile(w), r, epilogue=_C.EPI_RESID, y_ssq=ssq)
     d_ref = (x.float() @ w.float().t())
     torch.cuda.synchronize()
     d = d_ref.to(torch.bfloat16).float()
@@ -167,7 +177,7 @@ def test_residual_epilogue(device, m, k):
     assert torch.allclose(ssq, _tile_ssq(r), rtol=1e-5, atol=1e-6)
     # and the same as the standalone residual-add kernel applied to the projection
     r2 = r0.clone()
-    _C.add_rms_norm(_C.linear(x, w), r2, torch.ones(n, dtype=torch.bfloat16, device=device),
+    _C.add_rms_norm(_C.linear(x, _C.tile(w)), r2, torch.ones(n, dtype=torch.bfloat16, device=device),
                     torch.empty_like(r2), 1e-6)
     torch.cuda.synchronize()
     assert ((r.float() - r2.float()).abs() <= bound).all()
@@ -195,7 +205,7 @@ def test_split_k_is_deterministic_and_leaves_workspace_zero(device):
     for rep in range(3):
         for k in (2048, 3072):
             x, w = _operands(32, 1024, k, device, seed=k)
-            outs.append((rep, k, _C.linear(x, w, workspace=ws)))
+            outs.append((rep, k, _C.linear(x, _C.tile(w), workspace=ws)))
     torch.cuda.synchronize()
     by_k = {}
     for rep, k, y in outs:
@@ -210,23 +220,25 @@ def test_graph_replays_equal_eager(device):
     """A captured decode-style chain (norm prologue, SiLU, residual) replays to the eager result."""
     m, h, inter = 32, 1024, 3072
     gen = torch.Generator(device=device).manual_seed(8)
-    w_gu = (torch.randn((2 * inter, h), generator=gen, device=device) * 0.02).to(torch.bfloat16)
-    w_dn = (torch.randn((h, inter), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+    w_gu = _C.tile((torch.randn((2 * inter, h), generator=gen, device=device) * 0.02).to(torch.bfloat16))
+    w_dn = _C.tile((torch.randn((h, inter), generator=gen, device=device) * 0.02).to(torch.bfloat16))
     nw = (1.0 + 0.02 * torch.randn(h, generator=gen, device=device)).to(torch.bfloat16)
     ws = torch.zeros(max(_C.skinny_linear_workspace_size(inter, h, 1), _C.skinny_linear_workspace_size(h, inter, 2)),
                      dtype=torch.uint8, device=device)
-    r = torch.empty((m, h), dtype=torch.bfloat16, device=device)
+    r = _C.tiled_empty(m, h, device)  # the residual stream and the SiLU output tiled, as the model keeps them
     ssq = torch.empty((m, h // 32), device=device)
-    act = torch.empty((m, inter), dtype=torch.bfloat16, device=device)
+    act = _C.tiled_empty(m, inter, device)
 
     def chain():
-        _C.skinny_linear(r, w_gu, act, epilogue=_C.EPI_SILU, x_ssq=ssq, norm_weight=nw, workspace=ws)
-        _C.skinny_linear(act, w_dn, r, epilogue=_C.EPI_RESID, y_ssq=ssq, workspace=ws)
+        _C.skinny_linear(r, w_gu, act, epilogue=_C.EPI_SILU, x_ssq=ssq, norm_weight=nw, workspace=ws, m=m,
+                         y_tiled=True)
+        _C.skinny_linear(act, w_dn, r, epilogue=_C.EPI_RESID, y_ssq=ssq, workspace=ws, m=m, y_tiled=True)
 
     def reset(seed):
         g = torch.Generator(device=device).manual_seed(seed)
-        r.copy_(torch.randn((m, h), generator=g, device=device).to(torch.bfloat16))
-        ssq.copy_(_tile_ssq(r))
+        x = torch.randn((m, h), generator=g, device=device).to(torch.bfloat16)
+        r.copy_(_C.tile(x))
+        ssq.copy_(_tile_ssq(x))
 
     reset(1)
     chain()  # warm-up outside the capture
@@ -243,3 +255,60 @@ def test_graph_replays_equal_eager(device):
         chain()
         torch.cuda.synchronize()
         assert torch.equal(got_r, r) and torch.equal(got_ssq, ssq)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 13, 17, 32])
+@pytest.mark.parametrize("epi", [_C.EPI_STORE, _C.EPI_SILU, _C.EPI_RESID], ids=["store", "silu", "resid"])
+def test_tiled_activations_equal_row_major(device, m, epi):
+    """The same projection with x and y tiled gives the row-major results bit for bit (the same
+    fragments in the same order); padding rows of a tiled x -- here NaN -- reach only dropped
+    outputs, and padding rows of a tiled y are never written."""
+    n, k = {_C.EPI_STORE: (4096, 1024), _C.EPI_SILU: (3072, 1024), _C.EPI_RESID: (1024, 3072)}[epi]
+    wrows = 2 * n if epi == _C.EPI_SILU else n
+    x, w = _operands(m, wrows, k, device, seed=200 + m + epi)
+    wt = _C.tile(w)
+    rows = 16 * -(-m // 16)
+    norm = epi != _C.EPI_RESID
+    gen = torch.Generator(device=device).manual_seed(11)
+    nw = (1.0 + 0.02 * torch.randn(k, generator=gen, device=device)).to(torch.bfloat16) if norm else None
+    x_ssq = _tile_ssq(x).contiguous() if norm else None
+    ws = torch.zeros(max(_C.skinny_linear_workspace_size(n, k, epi), 16), dtype=torch.uint8, device=device)
+    x_pad = torch.full((rows, k), float("nan"), dtype=torch.bfloat16, device=device)
+    x_pad[:m] = x
+    xt = _C.tile(x_pad)
+    y_pad = torch.full((rows, n), 7.0, dtype=torch.bfloat16, device=device)  # sentinel rows past m
+    if epi == _C.EPI_RESID:
+        r0 = torch.randn((m, n), generator=gen, device=device).to(torch.bfloat16)
+        y_rm, ssq_rm = r0.clone(), torch.zeros((m, n // 32), device=device)
+        _C.skinny_linear(x, wt, y_rm, epilogue=epi, y_ssq=ssq_rm, workspace=ws)
+        y_pad[:m] = r0
+        yt = _C.tile(y_pad)
+        ssq_t = torch.zeros((m, n // 32), device=device)
+        _C.skinny_linear(xt, wt, yt, epilogue=epi, y_ssq=ssq_t, workspace=ws, m=m, y_tiled=True)
+        torch.cuda.synchronize()
+        assert torch.equal(ssq_t, ssq_rm)
+    else:
+        y_rm = _C.skinny_linear(x, wt, epilogue=epi, x_ssq=x_ssq, norm_weight=nw, workspace=ws)
+        yt = _C.tile(y_pad)
+        _C.skinny_linear(xt, wt, yt, epilogue=epi, x_ssq=x_ssq, norm_weight=nw, workspace=ws, m=m, y_tiled=True)
+        torch.cuda.synchronize()
+    got = _C.untile(yt)
+    assert torch.equal(got[:m], y_rm)
+    assert bool((got[m:] == 7.0).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 6, 16, 27])
+def test_embed_rows_tiled(device, rows):
+    gen = torch.Generator(device=device).manual_seed(12)
+    table = torch.randn((3000, 1024), generator=gen, device=device).to(torch.bfloat16)
+    ids = torch.randint(-2, 3002, (rows,), generator=gen, device=device)
+    ssq_rm, ssq_t = torch.zeros((rows, 32), device=device), torch.zeros((rows, 32), device=device)
+    ref = _C.embed_rows(ids, table, ssq=ssq_rm)
+    out = _C.tile(torch.full((16 * -(-rows // 16), 1024), 7.0, dtype=torch.bfloat16, device=device))
+    _C.embed_rows(ids, table, out=out, ssq=ssq_t, out_tiled=True)
+    torch.cuda.synchronize()
+    got = _C.untile(out)
+    assert torch.equal(got[:rows], ref) and torch.equal(ssq_t, ssq_rm)
+    assert bool((got[rows:] == 7.0).all())
