@@ -13,7 +13,8 @@
 //     ("tiled": 16 x 32 tiles of 512 elements, lane l's 8 elements at 8l), so one load
 //     instruction reads 1 KB of contiguous memory.  Against row-major operands (16 rows x
 //     64 bytes per instruction) this halves the vector L1 accesses that bound the
-//     M = 32 projections (qkv 6.4 -> 4.9 us).  Row-major X rows past M repeat row M-1;
+//     M = 32 projections (inside the decode step: qkv 7.0 -> 6.1 us, gate/up 8.3 -> 7.3 us).
+//     Row-major X rows past M repeat row M-1;
 //     a tiled X holds 16 * ceil(M/16) rows, and rows past M only reach dropped outputs;
 //   * a workgroup of NW waves owns 16*NT output columns and one of KS slices of K
 //     (split-K across workgroups where the column count alone gives too few
@@ -102,6 +103,8 @@ skinny_gemm_kernel(GemmArgs a) {
   constexpr int WK = 32 * KB;                           // K per wave per round
   constexpr int RK = kNW * WK;                          // K per workgroup per round
   constexpr int TF = 32 * 16;                           // floats of one 32-row x 16-column tile
+  static_assert(EPI != kEpiResid || CW % 32 == 0,
+                "the residual epilogue's sums of squares need whole 32-column groups in one workgroup");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -293,9 +296,11 @@ struct Plan {
 
 // Measured on MI355X at M = 32 (graph replay):
 //   * vocabulary-sized N (LM head): 128 columns per 4-wave workgroup, no split;
-//   * residual epilogue (N = hidden: o_proj, down_proj): 32 columns, K split over >= 256
-//     workgroups -- the deterministic cross-workgroup merge costs less than the X
-//     re-reads an unsplit K would need;
+//   * residual epilogue (N = hidden: o_proj, down_proj): 32 columns (the epilogue's sums of
+//     squares cover whole 32-column groups), K split over >= 256 workgroups.  Unsplit
+//     16-wave workgroups (32 of them) measure faster only while the weights sit in the
+//     Infinity Cache; streaming from HBM inside the decode step they take 8.2 us against
+//     6.9 / 7.7 us for the split o / down projections;
 //   * otherwise (qkv, gate_up): 16 columns per 8-wave workgroup, no split.
 Plan make_plan(int n, int k, int epi) {
   Plan p{8, 1, 1, k % 512 == 0 ? 2 : 1};

@@ -80,6 +80,23 @@ def test_fused_decode_step_argument_errors():
     assert _fused(lib, ws_bytes=16) == EWORKSPACE
 
 
+def test_skinny_linear_argument_errors():
+    lib = _C.load()
+
+    def call(**over):
+        args = dict(x=A, x_stride=1024, x_ssq=None, nw=None, eps=1e-6, w=A, y=A, y_stride=4096, y_ssq=None, epi=0,
+                    flags=0, m=32, n=4096, k=1024, ws=None, ws_bytes=0, stream=None)
+        args.update(over)
+        return lib.nvamd_skinny_linear(*args.values())
+
+    assert call(m=0) == 0
+    assert call(m=33) == EUNSUPPORTED                      # at most 32 rows
+    assert call(flags=4) == EINVAL                         # unknown flag
+    assert call(x_stride=1000) == EINVAL                   # row-major x rows shorter than k
+    assert call(w=A + 8) == EINVAL                         # the tiled weight is read 16 bytes at a time
+    assert call(epi=2, y_ssq=None) == EINVAL               # the residual epilogue writes sums of squares
+
+
 def test_paged_prefill_rejects_small_blocks():
     lib = _C.load()
     common = dict(out=A, out_stride=2048, q=A, q_stride=2048, k_cache=A, v_cache=A, num_blocks=64)
