@@ -294,28 +294,28 @@ struct Plan {
   int nw, nt, ks, kb;
 };
 
-// Measured on MI355X at M = 32 (graph replay):
+// Measured on MI355X at M = 32: the decode step's projection sequence over 28 layers' own
+// weights (882 MB, streamed from HBM as in the model), replayed as one graph:
 //   * vocabulary-sized N (LM head): 128 columns per 4-wave workgroup, no split;
 //   * residual epilogue (N = hidden: o_proj, down_proj): 32 columns (the epilogue's sums of
-//     squares cover whole 32-column groups), K split over >= 256 workgroups.  Unsplit
-//     16-wave workgroups (32 of them) measure faster only while the weights sit in the
-//     Infinity Cache; streaming from HBM inside the decode step they take 8.2 us against
-//     6.9 / 7.7 us for the split o / down projections;
+//     squares cover whole 32-column groups) per 8-wave workgroup, K split over >= 128
+//     workgroups (o 6.5 us, down 6.6 us; 4-wave workgroups over >= 256: 6.7 / 7.4 us;
+//     unsplit 16-wave workgroups: 8.2 us, faster only while the weights sit in the
+//     Infinity Cache);
 //   * otherwise (qkv, gate_up): 16 columns per 8-wave workgroup, no split.
 Plan make_plan(int n, int k, int epi) {
   Plan p{8, 1, 1, k % 512 == 0 ? 2 : 1};
   if (epi == kEpiStore && n % 128 == 0 && n / 128 >= 512) {
     p = Plan{4, 8, 1, 2};
   } else if (epi == kEpiResid) {
-    p = Plan{4, 2, 1, 1};
+    p = Plan{8, 2, 1, 2};
     const int groups = n / 32;
     static const int kSlices[] = {1, 2, 3, 4, 6, 8, 12, 16};
     for (int ks : kSlices) {
-      if (k % ks != 0 || (k / ks) % 128 != 0) continue;
+      if (k % ks != 0 || (k / ks) % 64 != 0) continue;  // whole 64-wide wave blocks per slice
       p.ks = ks;
-      if (groups * ks >= 256) break;
+      if (groups * ks >= 128) break;
     }
-    p.kb = (k / p.ks) % 256 == 0 ? 2 : 1;
   }
   return p;
 }
@@ -347,7 +347,7 @@ int dispatch(const GemmArgs &a, const Plan &p, int grid, hipStream_t stream) {
     if (p.nw == 4 && p.nt == 8) return launch_kb<4, 8, EPI, NORM>(a, p, grid, stream);
   }
   if constexpr (EPI == kEpiResid) {
-    if (p.nw == 4 && p.nt == 2) return launch_kb<4, 2, EPI, NORM>(a, p, grid, stream);
+    if (p.nw == 8 && p.nt == 2) return launch_kb<8, 2, EPI, NORM>(a, p, grid, stream);
   } else {
     if (p.nw == 8 && p.nt == 1) return launch_kb<8, 1, EPI, NORM>(a, p, grid, stream);
   }
