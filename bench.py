@@ -288,22 +288,44 @@ def prefill_leg(args, device) -> dict:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / reps
 
+    def rotating(fn, sets):
+        # consecutive launches take different buffer sets (together well beyond the 256 MB
+        # Infinity Cache), so each launch streams its bytes from HBM
+        turn = [0]
+
+        def call():
+            fn(*sets[turn[0] % len(sets)])
+            turn[0] += 1
+        return call
+
     # ~20 launches (8 ms) of sustained MFMA work pass before the clocks settle
     us_attn = timed(lambda: _C.varlen_prefill(out, q, k, v, cu, max(lens), scale), 40, warmup=30)
-    us_store = timed(lambda: _C.kv_cache_write(k, v, kc, vc, slots), 40)
+    store_sets = [(k, v, kc, vc)] + [(k.clone(), v.clone(), torch.zeros_like(kc), torch.zeros_like(vc))
+                                     for _ in range(2)]
+    us_store = timed(rotating(lambda a, b, c, d: _C.kv_cache_write(a, b, c, d, slots), store_sets), 42)
+    # the ceiling for these byte streams: a plain device copy of the same bytes, rotating likewise
+    copy_sets = [(torch.empty(2 * k.numel(), dtype=k.dtype, device=device),
+                  torch.cat([x[0].reshape(-1), x[1].reshape(-1)])) for x in store_sets]
+    us_copy = timed(rotating(lambda d, s_: d.copy_(s_), copy_sets), 42)
+    copy_gbs = 2 * (2 * k.numel() * 2) / us_copy / 1e3  # K and V bytes read + written per copy
+    del copy_sets
 
     # per-head q/k RMSNorm + RoPE + KV store of the same tokens, on views into a fused
     # projection output [T, (16 + 2 * 8) * 128], in place
     from nano_vllm_ascend_amd.layers import RotaryEmbedding
 
     table = RotaryEmbedding(128, 40960, W.ROPE_THETA).cos_sin.to(device)
-    qkv = torch.randn(t, 32 * 128, generator=gen, device=device).bfloat16()
-    qv, kv_, vv = qkv[:, :2048].view(t, 16, 128), qkv[:, 2048:3072].view(t, 8, 128), qkv[:, 3072:].view(t, 8, 128)
     qw = (1.0 + 0.02 * torch.randn(128, generator=gen, device=device)).bfloat16()
     kw = (1.0 + 0.02 * torch.randn(128, generator=gen, device=device)).bfloat16()
     pos = torch.tensor([p for n in lens for p in range(n)], dtype=torch.int64, device=device)
-    us_norm = timed(lambda: _C.qk_norm_rope(qv, kv_, qw, kw, pos, table, W.RMS_EPS, v=vv, key_cache=kc,
-                                            value_cache=vc, slot_mapping=slots), 40)
+    norm_sets = []
+    for _, _, c1, c2 in store_sets:
+        qkv = torch.randn(t, 32 * 128, generator=gen, device=device).bfloat16()
+        norm_sets.append((qkv[:, :2048].view(t, 16, 128), qkv[:, 2048:3072].view(t, 8, 128),
+                          qkv[:, 3072:].view(t, 8, 128), c1, c2))
+    us_norm = timed(rotating(lambda a, b, c, d, e: _C.qk_norm_rope(a, b, qw, kw, pos, table, W.RMS_EPS, v=c,
+                                                                   key_cache=d, value_cache=e, slot_mapping=slots),
+                             norm_sets), 42)
     norm_bytes = t * ((16 + 8) * 128 * 2 * 2 + 8 * 128 * 2 + 2 * 8 * 128 * 2 + 16)
 
     # paged (prefix-hit) route: 32 prompts of 1024 cached + 1024 new tokens through block tables
@@ -330,7 +352,8 @@ def prefill_leg(args, device) -> dict:
                       "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
         "kv_store": {"kernel": "kv_cache_write_kernel", "us": round(us_store, 2), "bytes": store_bytes,
                      "gbs": round(store_bytes / us_store / 1e3, 1),
-                     "frac": round(store_bytes / us_store / 1e3 / HBM_PEAK_GBS, 4)},
+                     "frac": round(store_bytes / us_store / 1e3 / HBM_PEAK_GBS, 4),
+                     "device_copy_gbs": round(copy_gbs, 1)},
         "qk_norm_rope": {"kernel": "qk_norm_rope_kernel (with the KV store)", "us": round(us_norm, 2),
                          "bytes": norm_bytes, "gbs": round(norm_bytes / us_norm / 1e3, 1),
                          "frac": round(norm_bytes / us_norm / 1e3 / HBM_PEAK_GBS, 4)},
