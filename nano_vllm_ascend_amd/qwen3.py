@@ -234,7 +234,7 @@ class Qwen3ForCausalLM(nn.Module):
     def forward(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, is_prefill: bool,
                 logits_indices=None) -> CausalLMOutput:
         if not is_prefill and logits_indices is None and self.decode_fusable(input_ids_flat.shape[0]):
-            if not self._tiled_ready:
+            if not self._tiled_ready or self.lm_head_tiled.device != self.lm_head.device:
                 self.build_decode_weights()
             ws = self.gemm_workspace()
             residual, ssq = self.model.forward_decode_fused(input_ids_flat, position_ids_flat, kv_cache,
