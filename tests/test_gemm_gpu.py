@@ -158,9 +158,13 @@ def test_norm_prologue_matches_add_rms_norm_then_linear(device, m, nk):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m", [1, 32])
-@pytest.mark.parametrize("k", [2048, 3072], ids=["o_proj", "down_proj"])
-def test_residual_epilogue(device, m, k):
-    n = 1024
+@pytest.mark.parametrize("nk", [(1024, 2048), (1024, 3072), (1024, 1024), (2048, 4096), (4096, 1024)],
+                         ids=["o_proj", "down_proj", "split4_k1024", "split2_k4096", "unsplit_n4096"])
+def test_residual_epilogue(device, m, nk):
+    """The residual epilogue over the K splits the plan picks (4 for n = 1024, 2 for n = 2048, none
+    for n = 4096): fp32-reference bound, the sums of squares of what was written, and agreement
+    with the standalone residual-add kernel."""
+    n, k = nk
     x, w = _operands(m, n, k, device, seed=71 + k + m)
     gen = torch.Generator(device=device).manual_seed(6)
     r0 = torch.randn((m, n), generator=gen, device=device).to(torch.bfloat16)
