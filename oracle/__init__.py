@@ -11,6 +11,9 @@ attention_ref      fp32 torch-CPU paged decode, dense and paged causal varlen
                    prefill, KV store, per-head RMSNorm + rotate-half RoPE.
 block_manager_ref  plain-Python restatement of the reference BlockManager,
                    including the per-token slot loop the GPU packing replaces.
+qwen3_ref          torch restatement of the reference Qwen3 forward (fp32, or
+                   bf16 at the reference's rounding points) for greedy-token
+                   and logits parity of the whole model.
 
 How each function is pinned (checked against something other than itself) is
 listed in the module docstrings and exercised by ``tests/test_oracle.py``.
