@@ -273,10 +273,10 @@ class BlockManager:
         return table[idx] * self.block_size + logical_pos % self.block_size
 
     # --------------------------------------------------------- GPU packing
-    def _ensure_mirror(self) -> torch.Tensor:
+    def _ensure_mirror(self, extra_width: int = 0) -> torch.Tensor:
         """Device mirror [rows, width]; doubles a dimension (keeping its contents) when outgrown."""
         need_rows = max(self._rows_used, 1)
-        need_width = max([len(t) for t in self.block_tables.values()] + [1])
+        need_width = max([len(t) for t in self.block_tables.values()] + [1]) + extra_width
         m = self._mirror
         if m is not None and m.shape[0] >= need_rows and m.shape[1] >= need_width:
             return m
@@ -292,12 +292,24 @@ class BlockManager:
         return new
 
     def _pack(self, slots, starts, qlens, token_ids=None, width: int | None = None,
-              out=None) -> PagedKVCacheMetadata:
-        """Ship descriptors + pending table entries (+ token ids) and expand them on the GPU."""
+              out=None, tentative: dict[tuple[int, int], int] | None = None) -> PagedKVCacheMetadata:
+        """Ship descriptors + pending table entries (+ token ids) and expand them on the GPU.
+
+        ``tentative`` maps (row, column) to blocks a decode step packed ahead of time will use
+        but the pool has not handed out yet: they are shipped and counted in the step's tables
+        and context lengths, and the host state is left as it is.
+        """
         b = len(slots)
         bs = self.block_size
         nblk = [len(self.block_tables[s]) for s in slots]
         ctx = [self.seq_lens[s] for s in slots]
+        if tentative:
+            extra_cols = {row: col for row, col in tentative}
+            for i, s in enumerate(slots):
+                col = extra_cols.get(self._row_of[s])
+                if col is not None:
+                    nblk[i] = col + 1
+            ctx = [max(c, st + n) for c, st, n in zip(ctx, starts, qlens)]
         for s, start, n, nb in zip(slots, starts, qlens, nblk):
             if start + n > nb * bs:
                 raise RuntimeError(f"missing block: slot={s}, logical_pos={start + n - 1}")
@@ -306,10 +318,12 @@ class BlockManager:
             if w > width:
                 raise RuntimeError(f"decode graph block table width {width} is smaller than runtime width {w}")
             w = width
-        mirror = self._ensure_mirror()
+        mirror = self._ensure_mirror(1 if tentative else 0)
         total = int(sum(qlens))
         pending = self._pending
         self._pending = {}
+        if tentative:
+            pending = {**pending, **tentative}
         n_up = len(pending)
         n_tok = total if token_ids is not None else 0
         arr = np.empty(5 * b + 3 * n_up + n_tok, dtype=np.int32)
@@ -400,3 +414,72 @@ class BlockManager:
                 self.seq_lens[slot] = end
         return self._pack(slots, list(start_positions), [q_len] * len(slots), token_ids=token_ids, width=width,
                           out=out)
+
+    # ------------------------------------------------ decode packed ahead of time
+    def peek_decode_blocks(self, slots: list[int], start_positions: list[int],
+                           q_len: int = 1) -> list[tuple[int, int]] | None:
+        """The blocks ``prepare_decode_metadata(slots, start_positions, q_len)`` would allocate,
+        as (slot, block id) in allocation order, without allocating them.
+
+        None when such a step must not be packed ahead of its confirmation: the pool would run
+        dry (the real call raises), or a block it would take still carries a prefix-cache key
+        (a tentative write into it could corrupt content a later prefix hit reads).
+        """
+        want = []
+        for slot, start in zip(slots, start_positions):
+            have = len(self.block_tables[slot])
+            want.extend([slot] * max(0, self._num_required_blocks(start + q_len) - have))
+        if len(want) > len(self._free):
+            return None
+        taken = []
+        for slot, block_id in zip(want, self._free):
+            if self.blocks[block_id].block_hash is not None:
+                return None
+            taken.append((slot, block_id))
+        return taken
+
+    def prepare_decode_ahead(self, slots: list[int], start_positions: list[int], token_ids=None,
+                             width: int | None = None, out=None):
+        """Pack a one-token decode step whose batch is not confirmed yet.
+
+        The step's metadata is exactly what ``prepare_decode_metadata`` will produce if nothing
+        touches the pool before it is called with the same batch: its new blocks are the front
+        of the free queue in batch order (``peek_decode_blocks``).  The pool, the tables and the
+        context lengths are left unchanged; ``commit_decode_ahead`` applies the step once it is
+        confirmed, and an unconfirmed step is simply forgotten.  Returns (metadata, taken), or
+        None when the step cannot be packed ahead (see ``peek_decode_blocks``, or a graph width
+        the step would outgrow).
+        """
+        if len(slots) != len(start_positions):
+            raise ValueError("slots and start_positions length mismatch")
+        taken = self.peek_decode_blocks(slots, start_positions, 1)
+        if taken is None:
+            return None
+        tentative: dict[tuple[int, int], int] = {}
+        for slot, block_id in taken:
+            row = self._row_of[slot]
+            col = len(self.block_tables[slot]) + sum(1 for (r, _) in tentative if r == row)
+            tentative[(row, col)] = block_id
+        if any(col > 0 and (r, col - 1) in tentative for (r, col) in tentative):
+            return None  # two new blocks for one sequence: only one-token steps are packed ahead
+        if width is not None and any(col >= width for (_, col) in tentative):
+            return None
+        if width is not None and any(len(self.block_tables[s]) > width for s in slots):
+            return None
+        md = self._pack(slots, list(start_positions), [1] * len(slots), token_ids=token_ids, width=width,
+                        out=out, tentative=tentative)
+        return md, taken
+
+    def commit_decode_ahead(self, slots: list[int], start_positions: list[int],
+                            taken: list[tuple[int, int]]) -> None:
+        """Apply a confirmed step packed by ``prepare_decode_ahead``: allocate as
+        ``prepare_decode_metadata`` does (same order, so the same blocks) and check that."""
+        before = {slot: len(self.block_tables[slot]) for slot, _ in taken}
+        for slot, start in zip(slots, start_positions):
+            end = start + 1
+            self.ensure_blocks(slot, end)
+            if end > self.seq_lens[slot]:
+                self.seq_lens[slot] = end
+        got = [(slot, self.block_tables[slot][before[slot]]) for slot, _ in taken]
+        if got != list(taken):
+            raise RuntimeError(f"decode step packed ahead used blocks {taken}, the pool handed out {got}")

@@ -8,16 +8,24 @@ Differences from the reference, all on the hot path:
     buffers, so a replay needs no device-to-device input copies;
   - greedy sampling of a batch is one argmax and ONE device-to-host read per
     step (the reference synchronised once per sequence);
-  - overlapped decode: when step N+1's inputs are fully determined before
-    step N's tokens reach the host (every sequence continues, nothing was
-    prefilled in between, greedy sampling, a captured batch size), step N+1
-    is launched right behind step N with its input ids copied on the device
-    from step N's argmax.  The host then reads step N's tokens and runs the
-    scheduler while the GPU computes step N+1.  The next call checks that the
-    batch it was asked for is the one launched (same sequences, same
-    positions) and otherwise launches normally; a discarded step only
-    rewrote identical K/V values or slots of finished sequences.  Outputs are
-    those of the synchronous loop.
+  - overlapped decode: when step N+1's batch is predictable before step N's
+    tokens reach the host (every sequence continues unless it samples EOS,
+    nothing was prefilled in between, greedy sampling, a captured batch
+    size), step N+1 is launched right behind step N with its input ids copied
+    on the device from step N's argmax, and the host reads step N's tokens and
+    plans the next engine step while the GPU runs.  Step N+1 is packed ahead
+    WITHOUT touching the block pool: a sequence that crosses into a new block
+    uses the block the pool would hand out next (the front of the free queue
+    in batch order), which is the block the synchronous loop allocates if
+    nothing else touches the pool first.  The next ``decode`` call confirms
+    the step only for the same Sequence objects at the same positions, and
+    only then allocates (checking it gets those blocks); any ``prefill`` or
+    ``free_seq`` in between discards it first.  So block allocation, and with
+    it every block table and slot mapping, follows the synchronous order.  A
+    discarded step wrote K/V only into rows no live sequence has reached and
+    into free blocks that carry no prefix-cache key (others are never packed
+    ahead), and every later write to those rows is ordered after it on the
+    stream.
 """
 from __future__ import annotations
 
@@ -27,7 +35,7 @@ import numpy as np
 import torch
 
 from . import _C
-from .block_manager import BlockManager
+from .block_manager import BlockManager, PagedKVCacheMetadata
 from .config import load_config
 from .graph import DecodeGraphRunner
 from .layers import RotaryEmbedding, Sampler
@@ -56,14 +64,21 @@ class _TokenFetch:
 
 
 class _InFlightStep:
-    """A decode step launched ahead of the call that asks for it."""
+    """A decode step launched ahead of the call that asks for it (not yet applied to the pool)."""
 
-    def __init__(self, slots, positions, entry, fetch: _TokenFetch, logits: torch.Tensor):
-        self.slots = slots
+    def __init__(self, seqs, positions, taken, entry, fetch: _TokenFetch, logits: torch.Tensor, snapshot=None):
+        self.seqs = list(seqs)
+        self.slots = [seq.seq_id for seq in seqs]
         self.positions = positions
+        self.taken = taken          # (slot, block) the step packed before the pool handed them out
         self.entry = entry
         self.fetch = fetch
         self.logits = logits
+        self.snapshot = snapshot    # host copy of its metadata, kept only for a metadata hook
+
+    def matches(self, seqs, positions) -> bool:
+        return (len(seqs) == len(self.seqs) and all(a is b for a, b in zip(seqs, self.seqs))
+                and positions == self.positions)
 
 
 class TokenIdTokenizer:
@@ -100,13 +115,7 @@ class ModelRunner:
         self.sampler = Sampler()
         self.enable_prefix_cache = enable_prefix_cache
         self.enable_decode_graph = enable_decode_graph
-        self.last_logits: torch.Tensor | None = None
-        self.enable_overlap = enable_overlap
-        self._in_flight: _InFlightStep | None = None
-        self._prefilled_since_decode = False
-        self._fetch: dict[int, list] = {}      # batch size -> [two _TokenFetch, next index]
-        self._logits_keep: dict[int, torch.Tensor] = {}
-        self.overlap_stats = {"launched": 0, "used": 0, "discarded": 0}
+        self._init_step_state(enable_overlap)
         self.config = load_config(model_path)
         self.tokenizer = _load_tokenizer(model_path, self.config.eos_token_id)
 
@@ -124,6 +133,22 @@ class ModelRunner:
                 model=self.model, kv_cache=self.kv_cache,
                 batch_sizes=decode_graph_batch_sizes or DEFAULT_DECODE_GRAPH_BATCH_SIZES,
                 max_model_len=max_model_len, block_size=block_size)
+
+    def _init_step_state(self, enable_overlap: bool) -> None:
+        """Per-step bookkeeping: last logits, the step launched ahead, token fetch buffers."""
+        self.last_logits: torch.Tensor | None = None
+        self.enable_overlap = enable_overlap
+        self._in_flight: _InFlightStep | None = None
+        self._prefilled_since_decode = False
+        self._fetch: dict[int, list] = {}      # batch size -> [two _TokenFetch, next index]
+        self._logits_keep: dict[int, torch.Tensor] = {}
+        self.overlap_stats = {"launched": 0, "used": 0, "discarded": 0}
+        # test hook: called as hook(kind, slots, metadata) with a host copy of the metadata of
+        # every prefill and every decode step that is actually taken
+        self.metadata_hook = None
+        # set by the engine's owner: whether the next engine step admits a waiting request (its
+        # batch then differs, so no step is launched ahead)
+        self.next_step_admits = None
 
     @torch.inference_mode()
     def _load_model(self, seed: int) -> Qwen3ForCausalLM:
@@ -198,15 +223,39 @@ class ModelRunner:
         return [int(self.sampler.sample(logits[i : i + 1], seq.sampling_params).item()) for i, seq in enumerate(seqs)]
 
     # ------------------------------------------------------------- forward
+    def _drop_in_flight(self) -> None:
+        """Forget a step launched ahead: the batch it assumed is not the next one."""
+        if self._in_flight is not None:
+            self._in_flight = None
+            self.overlap_stats["discarded"] += 1
+
+    @staticmethod
+    def _host_metadata(md) -> PagedKVCacheMetadata:
+        """A host copy (never a view: static graph buffers are overwritten by the next step)."""
+        def host(t):
+            return t.to("cpu", copy=True)
+
+        return PagedKVCacheMetadata(block_tables=host(md.block_tables), context_lens=host(md.context_lens),
+                                    slot_mapping=host(md.slot_mapping),
+                                    actual_seq_lengths_q=md.actual_seq_lengths_q,
+                                    actual_seq_lengths_kv=md.actual_seq_lengths_kv,
+                                    use_paged_prefill=md.use_paged_prefill)
+
+    def _report(self, kind: str, slots, md, is_host_copy: bool = False) -> None:
+        if self.metadata_hook is not None:
+            self.metadata_hook(kind, list(slots), md if is_host_copy else self._host_metadata(md))
+
     @torch.inference_mode()
     def prefill(self, seqs: list[Sequence]) -> None:
         if not seqs:
             return
+        self._drop_in_flight()
         self._prefilled_since_decode = True
         md = self.block_manager.prepare_prefill_metadata(
             slots=[s.seq_id for s in seqs], seq_lens=[s.runtime_prompt_len for s in seqs],
             start_positions=[s.cached_prefix_len for s in seqs], prefix_block_ids=[s.cached_block_ids for s in seqs],
             token_ids=[np.asarray(s.runtime_prompt_token_ids) for s in seqs])
+        self._report("prefill", [s.seq_id for s in seqs], md)
         out = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions, kv_cache=self.kv_cache,
                          attn_metadata=md, is_prefill=True, logits_indices=md.last_token_indices)
         self.last_logits = out.logits  # rows in `seqs` order; a graph replay reuses this buffer
@@ -234,12 +283,11 @@ class ModelRunner:
         return keep
 
     def _can_launch_ahead(self, seqs: list[Sequence]) -> bool:
-        # the next engine step decodes exactly these sequences when none finishes on a length
-        # limit or takes its final-token commit (engine.py), nothing was prefilled since the
-        # last decode (checked by the caller), and no EOS appears (unknown until the tokens are
-        # read: a miss is detected on the next call)
+        # the next engine step decodes exactly these sequences when none samples EOS (unknown
+        # until the tokens are read: the next call then discards the launch), none takes its
+        # final-token commit (engine.py) and nothing is admitted or prefilled in between
         return self.enable_overlap and all(
-            seq.sampling_params.is_greedy() and len(seq.generated_token_ids) + 1 < seq.max_new_tokens for seq in seqs)
+            seq.sampling_params.is_greedy() and not seq.pending_is_last() for seq in seqs)
 
     @torch.inference_mode()
     def decode(self, seqs: list[Sequence]) -> None:
@@ -252,16 +300,23 @@ class ModelRunner:
         graph = self.decode_graph_runner
         ahead, self._in_flight = self._in_flight, None
         entry = fetch = logits = None
-        if ahead is not None and ahead.slots == slots and ahead.positions == positions:
-            entry, fetch, logits = ahead.entry, ahead.fetch, ahead.logits  # launched by the previous call
+        reported = False
+        if ahead is not None and ahead.matches(seqs, positions):
+            # launched by the previous call: apply it to the pool now that the batch is confirmed
+            self.block_manager.commit_decode_ahead(ahead.slots, ahead.positions, ahead.taken)
+            entry, fetch, logits = ahead.entry, ahead.fetch, ahead.logits
             self.overlap_stats["used"] += 1
+            if ahead.snapshot is not None:
+                self._report("decode", slots, ahead.snapshot, is_host_copy=True)
         else:
             if ahead is not None:
                 self.overlap_stats["discarded"] += 1
             if graph is not None and graph.supports(b):
                 entry = graph.entry_for(b, 1, self.device, self.block_size)
-                self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens, width=entry.width,
-                                                           out=entry.buffers)
+                md = self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens,
+                                                                width=entry.width, out=entry.buffers)
+                self._report("decode", slots, md)
+                reported = True
                 logits = graph.replay(entry)  # the static buffers now hold this step's inputs
                 if logits is None:
                     entry = None
@@ -270,32 +325,46 @@ class ModelRunner:
                     graph.stats.fallbacks += 1
             if entry is None:
                 md = self.block_manager.prepare_decode_metadata(slots, positions, 1, token_ids=tokens)
+                if not reported:
+                    self._report("decode", slots, md)
                 logits = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions,
                                     kv_cache=self.kv_cache, attn_metadata=md, is_prefill=False).logits
             elif all(seq.sampling_params.is_greedy() for seq in seqs):
                 fetch = self._fetch_tokens(b, entry.buffers["greedy_ids"])
         self._prefilled_since_decode, prefilled = False, self._prefilled_since_decode
-        if entry is not None and fetch is not None and self._can_launch_ahead(seqs) and not prefilled:
-            # launch step N+1 behind this one: same sequences, next positions, input ids = this
-            # step's argmax (device to device); this step's logits leave the static buffer first
-            logits = self._keep_logits(b, logits)
-            nxt = [p + 1 for p in positions]
-            self.block_manager.prepare_decode_metadata(slots, nxt, 1, token_ids=tokens, width=entry.width,
-                                                       out=entry.buffers)
-            entry.buffers["input_ids"].copy_(entry.buffers["greedy_ids"])
-            nxt_logits = graph.replay(entry)
-            self._in_flight = _InFlightStep(slots, nxt, entry, self._fetch_tokens(b, entry.buffers["greedy_ids"]),
-                                            nxt_logits)
-            self.overlap_stats["launched"] += 1
+        admits = self.next_step_admits is not None and self.next_step_admits()
+        if entry is not None and fetch is not None and not prefilled and not admits and self._can_launch_ahead(seqs):
+            logits = self._launch_ahead(seqs, positions, tokens, entry, logits)
         self.last_logits = logits
         ids = fetch.tokens() if fetch is not None else self._sample(logits, seqs)
         for seq, token in zip(seqs, ids):
             seq.set_decode_result(token)
 
+    def _launch_ahead(self, seqs, positions, tokens, entry, logits) -> torch.Tensor:
+        """Launch step N+1 behind step N: same sequences, next positions, input ids = step N's
+        argmax (device to device).  Returns step N's logits, copied out of the static buffer
+        the launched replay overwrites (unchanged when nothing is launched)."""
+        b = len(seqs)
+        nxt = [p + 1 for p in positions]
+        packed = self.block_manager.prepare_decode_ahead([seq.seq_id for seq in seqs], nxt, token_ids=tokens,
+                                                         width=entry.width, out=entry.buffers)
+        if packed is None:
+            return logits
+        md, taken = packed
+        kept = self._keep_logits(b, logits)
+        snapshot = self._host_metadata(md) if self.metadata_hook is not None else None
+        entry.buffers["input_ids"].copy_(entry.buffers["greedy_ids"])
+        nxt_logits = self.decode_graph_runner.replay(entry)
+        self._in_flight = _InFlightStep(seqs, nxt, taken, entry, self._fetch_tokens(b, entry.buffers["greedy_ids"]),
+                                        nxt_logits, snapshot)
+        self.overlap_stats["launched"] += 1
+        return kept
+
     def decode_graph_stats(self) -> dict[str, int]:
         return {} if self.decode_graph_runner is None else self.decode_graph_runner.stats_dict()
 
     def free_seq(self, seq: Sequence) -> None:
+        self._drop_in_flight()  # a finishing sequence was in the launched batch
         self.block_manager.free_slot(seq.seq_id)
 
     def clear_prefix_cache(self) -> None:

@@ -1,13 +1,20 @@
-"""Per-request state (nv/sequence.py:14-67).
+"""Per-request state of the continuous-batching engine.
 
-Packing reads ``cached_prefix_len``, ``cached_block_ids``,
-``runtime_prompt_token_ids/len``, ``cache_position`` and ``next_token_id``.
-The position of the token fed to a decode step is ``cache_position`` =
-prompt_len + number of decode steps already run.
+The model runner talks to a request through the attribute and method names of
+nv/sequence.py:20-67 (the prefix-cache plan fields, ``set_prefill_result``,
+``append_next_token``, ``set_decode_result``, ``cache_position``,
+``next_token_id``, ``generated_token_ids``); those names are the interface.
+The representation is this module's own:
+
+  * a request moves WAITING -> RUNNING -> FINISHED (``status``);
+  * after its prefill it always holds exactly one sampled token that is not
+    yet part of its output (``next_token_id``, ``None`` before the prefill);
+  * a decode step commits that token to the output, feeds it to the model at
+    ``cache_position`` and receives the next one, so ``cache_position`` is
+    derived, not stored: prompt_len + decode steps taken.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass, field
 from enum import Enum
 from typing import Any
 
@@ -18,49 +25,80 @@ class SequenceStatus(str, Enum):
     FINISHED = "finished"
 
 
-@dataclass
 class Sequence:
-    seq_id: int
-    prompt: str
-    max_new_tokens: int
-    prompt_token_ids: Any  # 1-D int tensor or list of token ids
-    sampling_params: Any
+    __slots__ = (
+        "seq_id", "prompt", "max_new_tokens", "prompt_token_ids", "sampling_params",
+        "status", "finish_reason", "reserved_blocks",
+        # prefix-cache plan, filled at submit time by the runner
+        "estimated_prompt_len", "cached_prefix_len", "cached_block_ids", "runtime_prompt_token_ids",
+        "runtime_prompt_len",
+        # generation state
+        "prompt_len", "generated_token_ids", "_pending", "_decode_steps",
+    )
 
-    status: SequenceStatus = SequenceStatus.WAITING
-    estimated_prompt_len: int = 0
-    reserved_blocks: int = 0
-    finish_reason: str | None = None
-    cached_prefix_len: int = 0
-    cached_block_ids: list[int] = field(default_factory=list)
-    runtime_prompt_token_ids: Any = None
-    runtime_prompt_len: int = 0
+    def __init__(self, seq_id: int, prompt: str, max_new_tokens: int, prompt_token_ids: Any, sampling_params: Any):
+        self.seq_id = seq_id
+        self.prompt = prompt
+        self.max_new_tokens = max_new_tokens
+        self.prompt_token_ids = prompt_token_ids
+        self.sampling_params = sampling_params
+        self.status = SequenceStatus.WAITING
+        self.finish_reason: str | None = None
+        self.reserved_blocks = 0
+        self.estimated_prompt_len = 0
+        self.cached_prefix_len = 0
+        self.cached_block_ids: list[int] = []
+        self.runtime_prompt_token_ids = None
+        self.runtime_prompt_len = 0
+        self.prompt_len = 0
+        self.generated_token_ids: list[int] = []
+        self._pending: int | None = None
+        self._decode_steps = 0
 
-    # set by prefill
-    prompt_len: int = 0
-    cache_position: int = 0
-    next_token_id: int | None = None
+    def __repr__(self) -> str:
+        return (f"Sequence(id={self.seq_id}, {self.status.value}, out={len(self.generated_token_ids)}"
+                f"/{self.max_new_tokens}, pending={self._pending})")
 
-    # generated tokens only (no prompt tokens)
-    generated_token_ids: list[int] = field(default_factory=list)
+    # ------------------------------------------------------------ derived
+    @property
+    def next_token_id(self) -> int | None:
+        """The sampled token not yet committed to the output (None before the prefill)."""
+        return self._pending
 
-    def set_prefill_result(self, next_token_id: int, prompt_len: int) -> None:
-        self.next_token_id = next_token_id
-        self.prompt_len = prompt_len
-        self.cache_position = prompt_len
+    @property
+    def cache_position(self) -> int:
+        """Position of the token the next decode step feeds: prompt_len + decode steps taken."""
+        return self.prompt_len + self._decode_steps
 
-    def append_next_token(self) -> int:
-        """Commit the pending sampled token to the output and return it."""
-        if self.next_token_id is None:
-            raise RuntimeError(f"seq {self.seq_id} has no next_token_id")
-        self.generated_token_ids.append(self.next_token_id)
-        return self.next_token_id
+    @property
+    def tokens_left(self) -> int:
+        """Output tokens still to commit, counting the pending one."""
+        return self.max_new_tokens - len(self.generated_token_ids)
 
-    def set_decode_result(self, next_token_id: int) -> None:
-        self.next_token_id = next_token_id
-        self.cache_position += 1
+    def pending_is_last(self) -> bool:
+        """Committing the pending token fills the output budget, so it needs no forward."""
+        return self.tokens_left <= 1
 
     def reach_max_tokens(self) -> bool:
-        return len(self.generated_token_ids) >= self.max_new_tokens
+        return self.tokens_left <= 0
+
+    # ------------------------------------------------------------ transitions
+    def set_prefill_result(self, next_token_id: int, prompt_len: int) -> None:
+        self.prompt_len = prompt_len
+        self._decode_steps = 0
+        self._pending = next_token_id
+
+    def append_next_token(self) -> int:
+        """Move the pending token into the output; return it."""
+        token = self._pending
+        if token is None:
+            raise RuntimeError(f"seq {self.seq_id} has no next_token_id")
+        self.generated_token_ids.append(token)
+        return token
+
+    def set_decode_result(self, next_token_id: int) -> None:
+        self._decode_steps += 1
+        self._pending = next_token_id
 
     def finish(self, reason: str | None = None) -> None:
         self.status = SequenceStatus.FINISHED

@@ -22,20 +22,23 @@ from .attention_ref import rope_cos_sin_table
 
 
 class Qwen3Ref:
-    def __init__(self, state: dict, config, round_bf16: bool = True, max_positions: int = 4096):
+    def __init__(self, state: dict, config, round_bf16: bool = True, max_positions: int = 4096, device="cpu"):
+        """``device``: where the fp32 arithmetic runs (the CPU, or a GPU for the full-depth model)."""
         self.cfg = config
         self.rb = round_bf16
-        self.w = {k: v.detach().to("cpu", torch.float32) for k, v in state.items()}
+        self.device = torch.device(device)
+        self.w = {k: v.detach().to(self.device, torch.float32) for k, v in state.items()}
         cos, sin = rope_cos_sin_table(config.head_dim, max_positions, config.rope_theta)
         if round_bf16:  # the reference casts the fp32 table to the activation dtype
             cos, sin = cos.to(torch.bfloat16).float(), sin.to(torch.bfloat16).float()
-        self.cos, self.sin = cos, sin
+        self.cos, self.sin = cos.to(self.device), sin.to(self.device)
         self.reset()
 
     def reset(self):
         n = self.cfg.num_hidden_layers
-        self.k_cache = [torch.zeros(0, self.cfg.num_key_value_heads, self.cfg.head_dim) for _ in range(n)]
-        self.v_cache = [torch.zeros(0, self.cfg.num_key_value_heads, self.cfg.head_dim) for _ in range(n)]
+        shape = (0, self.cfg.num_key_value_heads, self.cfg.head_dim)
+        self.k_cache = [torch.zeros(shape, device=self.device) for _ in range(n)]
+        self.v_cache = [torch.zeros(shape, device=self.device) for _ in range(n)]
         self.pos = 0
 
     def _r(self, x):
@@ -57,8 +60,8 @@ class Qwen3Ref:
         """Append tokens to the cache; return fp32 logits of the last one."""
         cfg, w = self.cfg, self.w
         t = len(token_ids)
-        pos = torch.arange(self.pos, self.pos + t)
-        h = w["model.embed_tokens"][torch.tensor(token_ids)]
+        pos = torch.arange(self.pos, self.pos + t, device=self.device)
+        h = w["model.embed_tokens"][torch.tensor(token_ids, device=self.device)]
         hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         qs, kvs = hq * d, hkv * d
         for i in range(cfg.num_hidden_layers):
@@ -74,10 +77,12 @@ class Qwen3Ref:
             self.v_cache[i] = torch.cat([self.v_cache[i], v])
             kk = self.k_cache[i].repeat_interleave(hq // hkv, dim=1)
             vv = self.v_cache[i].repeat_interleave(hq // hkv, dim=1)
-            s = torch.einsum("qhd,khd->hqk", q, kk) * d ** -0.5
-            keys = torch.arange(kk.shape[0])
+            # [h, q, d] @ [h, d, k] and [h, q, k] @ [h, k, d], contiguous fp32 operands
+            s = torch.matmul(q.transpose(0, 1).contiguous(), kk.permute(1, 2, 0).contiguous()) * d ** -0.5
+            keys = torch.arange(kk.shape[0], device=self.device)
             s = s.masked_fill(keys[None, None, :] > pos[None, :, None], float("-inf"))
-            a = self._r(torch.einsum("hqk,khd->qhd", torch.softmax(s, -1), vv)).reshape(t, qs)
+            pv = torch.matmul(torch.softmax(s, -1), vv.transpose(0, 1).contiguous())
+            a = self._r(pv.transpose(0, 1)).reshape(t, qs)
             h = self._r(h + self._r(a @ w[p + "self_attn.o_weight"].T))
             x = self._norm(h, w[p + "post_attention_layernorm.weight"])
             gu = self._r(x @ w[p + "mlp.gate_up_weight"].T)

@@ -16,7 +16,6 @@ from pathlib import Path
 import pytest
 import torch
 
-from nano_vllm_ascend_amd.block_manager import BlockManager, PagedKVCacheMetadata
 from nano_vllm_ascend_amd.engine import EngineCore
 from nano_vllm_ascend_amd.sampling_params import SamplingParams
 from nano_vllm_ascend_amd.scheduler import MiniScheduler
@@ -26,22 +25,7 @@ from oracle.block_manager_ref import BlockManagerRef
 GOLDEN = Path(__file__).resolve().parent / "golden"
 sys.path.insert(0, str(GOLDEN))
 import trace_driver  # noqa: E402
-
-
-class HostPackedBlockManager(BlockManager):
-    """Test double: metadata from host state (closed form), state machine untouched."""
-
-    def _pack(self, slots, starts, qlens, token_ids=None, width=None, out=None):
-        bs = self.block_size
-        nblk = [len(self.block_tables[s]) for s in slots]
-        w = max(nblk) if width is None else width
-        bt = torch.zeros((len(slots), w), dtype=torch.int32)
-        for i, s in enumerate(slots):
-            bt[i, : nblk[i]] = torch.tensor(self.block_tables[s], dtype=torch.int32)
-        sm = [self._physical_slot(s, st + k) for s, st, n in zip(slots, starts, qlens) for k in range(n)]
-        ctx = [self.seq_lens[s] for s in slots]
-        return PagedKVCacheMetadata(block_tables=bt, context_lens=torch.tensor(ctx, dtype=torch.int32),
-                                    slot_mapping=torch.tensor(sm, dtype=torch.int64), context_lens_host=ctx)
+from host_pack import HostPackedBlockManager  # noqa: E402
 
 
 MANAGERS = [BlockManagerRef, HostPackedBlockManager]
