@@ -302,14 +302,15 @@ class BlockManager:
         b = len(slots)
         bs = self.block_size
         nblk = [len(self.block_tables[s]) for s in slots]
-        ctx = [self.seq_lens[s] for s in slots]
+        # a step's context ends at its last token; the recorded length already covers it, except
+        # for a step packed ahead of its confirmation
+        ctx = [max(self.seq_lens[s], st + n) for s, st, n in zip(slots, starts, qlens)]
         if tentative:
             extra_cols = {row: col for row, col in tentative}
             for i, s in enumerate(slots):
                 col = extra_cols.get(self._row_of[s])
                 if col is not None:
                     nblk[i] = col + 1
-            ctx = [max(c, st + n) for c, st, n in zip(ctx, starts, qlens)]
         for s, start, n, nb in zip(slots, starts, qlens, nblk):
             if start + n > nb * bs:
                 raise RuntimeError(f"missing block: slot={s}, logical_pos={start + n - 1}")

@@ -7,6 +7,7 @@ import sys
 from collections import OrderedDict
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -128,3 +129,43 @@ def test_prefix_hit_prefill_packing(device):
     assert torch.equal(b.block_tables.cpu(), a.block_tables)
     assert torch.equal(b.slot_mapping.cpu(), a.slot_mapping)
     assert b.positions.cpu().tolist() == [40, 41, 42] + list(range(7))
+
+
+@pytest.mark.gpu
+def test_decode_step_packed_ahead_equals_the_confirmed_step(device):
+    """A decode step packed ahead of its confirmation (GPU packing with tentative blocks for the
+    sequences that open a block) equals, bit for bit, the metadata prepare_decode_metadata packs
+    for the same step after the confirmation, and leaves the pool untouched until then."""
+    rng = random.Random(7)
+    ref, bm = _seeded_pair(256, 128, seed=7, device=device)
+    lens = [127, 128, 129, 255, 256, 300, 511, 1, 64, 383]  # several open a block at the next position
+    slots = list(range(len(lens)))
+    bm.prepare_prefill_metadata(slots, lens, [0] * len(lens), [[] for _ in slots])
+    ref.prepare_prefill_metadata(slots, lens, [0] * len(lens), [[] for _ in slots])
+    width = 8
+    for step in range(3):
+        pos = [n + step for n in lens]
+        bufs = {k: torch.full((len(slots), width) if k == "block_tables" else (len(slots) + (k == "cu_seqlens_q"),),
+                              -7, dtype=torch.int32 if k in ("block_tables", "context_lens", "cu_seqlens_q")
+                              else torch.int64, device=device)
+                for k in ("block_tables", "context_lens", "slot_mapping", "positions", "cu_seqlens_q",
+                          "last_token_indices", "input_ids")}
+        free_before = list(bm.free_block_ids)
+        toks = np.array([rng.randint(0, 1000) for _ in slots], dtype=np.int64)
+        md, taken = bm.prepare_decode_ahead(slots, pos, token_ids=toks, width=width, out=bufs)
+        torch.cuda.synchronize()
+        got = {k: v.cpu().clone() for k, v in bufs.items()}
+        assert bm.free_block_ids == free_before
+        bm.commit_decode_ahead(slots, pos, taken)
+        want = bm.prepare_decode_metadata(slots, pos, 1, token_ids=toks, width=width)
+        r = ref.prepare_decode_metadata(slots, pos, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(got["block_tables"], want.block_tables.cpu())
+        assert torch.equal(got["block_tables"][:, : r.block_tables.shape[1]], r.block_tables)
+        for k, attr in (("context_lens", "context_lens"), ("slot_mapping", "slot_mapping"),
+                        ("positions", "positions"), ("input_ids", "input_ids")):
+            assert torch.equal(got[k], getattr(want, attr).cpu()), (step, k)
+        assert torch.equal(got["context_lens"], r.context_lens) and torch.equal(got["slot_mapping"], r.slot_mapping)
+        assert got["context_lens"].tolist() == [p + 1 for p in pos]
+        # step 0 writes positions 128 and 256 into new blocks; step 1 positions 128, 256, 384, 512
+        assert len(taken) == {0: 2, 1: 4, 2: 0}[step]
