@@ -35,6 +35,7 @@ extern "C" {
 #define NVAMD_EINVAL (-1)      /* a size, stride or pointer is invalid        */
 #define NVAMD_EUNSUPPORTED (-2) /* head_dim / GQA group / block_size not built */
 #define NVAMD_EWORKSPACE (-3)  /* workspace missing or too small               */
+#define NVAMD_ETOOLARGE (-4)   /* needs more than the library's static scratch  */
 
 /* ABI version of this header; nvamd_version() returns the version the library was built
    with, for the loader's sanity check. */
@@ -72,6 +73,29 @@ int nvamd_paged_decode(void *out, int64_t out_stride,
                        float scale, int max_context_len,
                        void *workspace, size_t workspace_bytes,
                        hipStream_t stream);
+
+/* Allocation-free variant of nvamd_paged_decode.  It has no counterpart in  */
+/* the reference: it is for callers that cannot allocate device memory      */
+/* (code under graph capture, tight serving loops, harnesses that forbid     */
+/* allocation).  Same arguments and results as nvamd_paged_decode, without  */
+/* the workspace: the library's own device array of                        */
+/* NVAMD_DECODE_SCRATCH_BYTES, one copy per GPU held until the process      */
+/* ends, serves as the workspace.  A call that would need more returns      */
+/* NVAMD_ETOOLARGE and launches nothing (the need is                        */
+/* nvamd_paged_decode_workspace_size(batch, ...); 64 MiB covers e.g. 100    */
+/* sequences x 4096 tokens or 32 x 8192 at 16 query / 8 KV heads).  The     */
+/* first call on a device also clears the array's counters on `stream`.     */
+/* All calls on one GPU share its array: calls that overlap on one GPU race. */
+#define NVAMD_DECODE_SCRATCH_BYTES (64u * 1024u * 1024u)
+int nvamd_paged_decode_noalloc(void *out, int64_t out_stride,
+                               const void *q, int64_t q_stride,
+                               const void *k_cache, const void *v_cache,
+                               int num_blocks, int block_size,
+                               const int32_t *block_tables, int bt_stride,
+                               int bt_width, const int32_t *context_lens,
+                               int batch, int num_heads, int num_kv_heads,
+                               int head_dim, float scale,
+                               int max_context_len, hipStream_t stream);
 
 /* ------------------------------------------------------------------------- */
 /* P5 + P2 + P4 fused: one decode step of a layer's attention.                */

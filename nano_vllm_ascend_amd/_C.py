@@ -17,7 +17,9 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libnvamd.so"
 
 NVAMD_OK = 0
-_ERRORS = {-1: "invalid argument", -2: "unsupported configuration", -3: "workspace missing or too small"}
+_ERRORS = {-1: "invalid argument", -2: "unsupported configuration", -3: "workspace missing or too small",
+           -4: "needs more than the library's static scratch (NVAMD_DECODE_SCRATCH_BYTES)"}
+DECODE_SCRATCH_BYTES = 64 * 1024 * 1024  # NVAMD_DECODE_SCRATCH_BYTES
 
 _c_int = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -33,6 +35,11 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_ptr,
          _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_ptr, _c_size, _c_ptr],
+    ),
+    "nvamd_paged_decode_noalloc": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_int, _c_ptr,
+         _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_ptr],
     ),
     "nvamd_paged_decode_fused": (
         _c_int,
@@ -163,6 +170,30 @@ def paged_decode(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, va
     int32 [B] on the device; max_context_len bounds every context_lens entry.
     """
     lib = load()
+    args = _decode_args(out, q, key_cache, value_cache, block_tables, context_lens, scale, max_context_len)
+    status = lib.nvamd_paged_decode(*args, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                                    _stream())
+    _check(status, "nvamd_paged_decode")
+    return out
+
+
+def paged_decode_noalloc(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                         block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                         max_context_len: int) -> torch.Tensor:
+    """``paged_decode`` without a workspace: the library's static per-GPU scratch serves as one.
+
+    Raises ValueError when the call needs more than DECODE_SCRATCH_BYTES
+    (paged_decode_workspace_size of its sizes).  Calls that overlap on one GPU share the
+    scratch and race.
+    """
+    lib = load()
+    args = _decode_args(out, q, key_cache, value_cache, block_tables, context_lens, scale, max_context_len)
+    _check(lib.nvamd_paged_decode_noalloc(*args, _stream()), "nvamd_paged_decode_noalloc")
+    return out
+
+
+def _decode_args(out, q, key_cache, value_cache, block_tables, context_lens, scale, max_context_len) -> tuple:
+    """Checked arguments of the decode entry points, up to the workspace."""
     _bf16_cuda("q", q)
     _bf16_cuda("out", out)
     _bf16_cuda("key_cache", key_cache)
@@ -179,14 +210,9 @@ def paged_decode(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, va
     _require(context_lens.dtype == torch.int32 and context_lens.numel() == b and context_lens.is_cuda,
              "context_lens must be int32 [B] on the device")
     _require(context_lens.is_contiguous(), "context_lens must be contiguous")
-    status = lib.nvamd_paged_decode(
-        out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), key_cache.data_ptr(),
-        value_cache.data_ptr(), nb, bs, block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
-        context_lens.data_ptr(), b, hq, hkv, d, float(scale), int(max_context_len), workspace.data_ptr(),
-        workspace.numel() * workspace.element_size(), _stream(),
-    )
-    _check(status, "nvamd_paged_decode")
-    return out
+    return (out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), key_cache.data_ptr(),
+            value_cache.data_ptr(), nb, bs, block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+            context_lens.data_ptr(), b, hq, hkv, d, float(scale), int(max_context_len))
 
 
 def paged_decode_fused(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

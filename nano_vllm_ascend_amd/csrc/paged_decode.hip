@@ -44,6 +44,8 @@
 // slots[b] -- one launch instead of qk_norm_rope + decode, with identical results: the
 // norm's partial sums are combined in the same balanced tree as the standalone kernel's.
 // The wave whose chunk holds the new token's row stores it before loading its chunk.
+#include <mutex>
+
 #include "common.h"
 
 namespace nvamd {
@@ -747,4 +749,72 @@ extern "C" int nvamd_paged_decode_fused(void *out, int64_t out_stride, const voi
   a.slots = slot_mapping;
   a.num_slots = (int64_t)num_blocks * block_size;
   return dispatch_gqa<true>(a, num_heads / num_kv_heads, batch, stream);
+}
+
+// -------------------------------------------------------------------------------------------
+// Allocation-free decode (nvamd_paged_decode_noalloc): the workspace of nvamd_paged_decode
+// comes from `scratch`, a file-scope device array of NVAMD_DECODE_SCRATCH_BYTES of which every
+// GPU the library runs on holds its own copy until the process ends.  In host code the array's
+// name is only a host-side stand-in, never an address: the first call on a device, with that
+// device current, asks hipGetSymbolAddress for that device's copy, keeps the address per
+// device, and clears the copy's arrival counters with a fill kernel on the caller's stream
+// (ordered before the call's own launch).  Every call leaves the counters at zero again, as it
+// does with a caller's workspace; partial results need no clearing.  Calls share the device's
+// copy: calls that can overlap on one GPU (several streams, several host threads) race on it.
+__device__ __align__(256) unsigned char scratch[NVAMD_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch[kMaxDevices];  // each device's address of `scratch`, set on its first call
+
+__global__ void __launch_bounds__(256) zero_words_kernel(u32 *p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// The current device's copy of `scratch`, set up (address looked up, counters cleared) on the
+// device's first call.
+int device_scratch(hipStream_t stream, void **ptr) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return (int)err;
+  if (dev < 0 || dev >= kMaxDevices) return NVAMD_EUNSUPPORTED;
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch[dev] == nullptr) {
+    void *p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return (int)err;
+    if (p == nullptr) return (int)hipErrorInvalidSymbol;
+    constexpr int words = (int)(kCounterBytes / sizeof(u32));
+    hipLaunchKernelGGL(zero_words_kernel, dim3(words / 256), dim3(256), 0, stream, static_cast<u32 *>(p), words);
+    const int st = launch_status();
+    if (st != NVAMD_OK) return st;
+    g_scratch[dev] = p;
+  }
+  *ptr = g_scratch[dev];
+  return NVAMD_OK;
+}
+
+static_assert(kCounterBytes % (256 * sizeof(u32)) == 0, "counter clear uses whole 256-thread blocks");
+static_assert(NVAMD_DECODE_SCRATCH_BYTES > kCounterBytes, "scratch must hold the counters and some partials");
+
+}  // namespace
+
+extern "C" int nvamd_paged_decode_noalloc(void *out, int64_t out_stride, const void *q, int64_t q_stride,
+                                          const void *k_cache, const void *v_cache, int num_blocks, int block_size,
+                                          const int32_t *block_tables, int bt_stride, int bt_width,
+                                          const int32_t *context_lens, int batch, int num_heads, int num_kv_heads,
+                                          int head_dim, float scale, int max_context_len, hipStream_t stream) {
+  if (batch == 0) return NVAMD_OK;
+  const size_t need = nvamd_paged_decode_workspace_size(batch, num_heads, num_kv_heads, max_context_len);
+  if (need == 0) return NVAMD_EINVAL;
+  if (need > (size_t)NVAMD_DECODE_SCRATCH_BYTES) return NVAMD_ETOOLARGE;
+  void *ws = nullptr;
+  const int st = device_scratch(stream, &ws);
+  if (st != NVAMD_OK) return st;
+  return nvamd_paged_decode(out, out_stride, q, q_stride, k_cache, v_cache, num_blocks, block_size, block_tables,
+                            bt_stride, bt_width, context_lens, batch, num_heads, num_kv_heads, head_dim, scale,
+                            max_context_len, ws, (size_t)NVAMD_DECODE_SCRATCH_BYTES, stream);
 }

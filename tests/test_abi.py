@@ -52,7 +52,7 @@ def test_build_rejects_kernels_that_spill_to_scratch():
 
 # Argument checks run on the host before any HIP call, so they are testable without a GPU.  The
 # addresses below are fake 16-byte-aligned device addresses that no failing call dereferences.
-EINVAL, EUNSUPPORTED, EWORKSPACE = -1, -2, -3
+EINVAL, EUNSUPPORTED, EWORKSPACE, ETOOLARGE = -1, -2, -3, -4
 A = 0x10000  # aligned stand-in address
 
 
@@ -104,3 +104,17 @@ def test_paged_prefill_rejects_small_blocks():
                 scale=128 ** -0.5, stream=None)
     for bs, want in ((8, EUNSUPPORTED), (12, EUNSUPPORTED)):
         assert lib.nvamd_paged_prefill(*common.values(), bs, *tail.values()) == want
+
+
+def test_noalloc_decode_size_limit_is_checked_on_the_host():
+    """The allocation-free decode refuses a call whose workspace would exceed the static scratch
+    before it touches the device (fake addresses, no GPU needed)."""
+    lib = _C.load()
+    header = HEADER.read_text()
+    assert "#define NVAMD_DECODE_SCRATCH_BYTES (64u * 1024u * 1024u)" in header
+    assert _C.DECODE_SCRATCH_BYTES == 64 * 1024 * 1024
+    args = [A, 2048, A, 2048, A, A, 64, 128, A, 8, 8, A, 4, 16, 8, 128, 128 ** -0.5]
+    assert lib.nvamd_paged_decode_noalloc(*args, 2_621_440, None) == ETOOLARGE
+    assert lib.nvamd_paged_decode_noalloc(*args[:12], 0, *args[13:], 1024, None) == 0  # empty batch
+    fits = _C.paged_decode_workspace_size(100, 16, 8, 4096)
+    assert fits <= _C.DECODE_SCRATCH_BYTES < _C.paged_decode_workspace_size(100, 16, 8, 8192)
