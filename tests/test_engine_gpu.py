@@ -34,9 +34,12 @@ def make_llm(graph=True, prefix=False, layers=SMALL, num_blocks=96, max_num_seqs
 # at most a tenth of the tokens differ.
 LOGIT_TOL = 0.08
 TIE_TOL = 0.05
-# the same bars for the 28-layer model, where the rounding differences compound over depth
-FULL_LOGIT_TOL = 0.25
-FULL_TIE_TOL = 0.15
+# The same bars for the 28-layer model, where rounding differences compound over depth: the
+# largest per-step logit difference measured on MI355X is 0.053, the largest mismatch margin 0.042
+# (1021/1056 tokens equal); the bars are twice the per-logit difference, and at least nine
+# tokens in ten must be equal.
+FULL_LOGIT_TOL = 0.1
+FULL_TIE_TOL = 0.1
 
 
 @pytest.mark.gpu
@@ -177,6 +180,7 @@ def test_full_depth_greedy_tokens_against_oracle(device):
           f"worst logit difference per step: {[round(w, 3) for w in worst]}")
     assert max(worst) <= FULL_LOGIT_TOL
     assert all(margin < FULL_TIE_TOL for _, _, margin, _ in mismatches), mismatches
+    assert len(mismatches) <= total // 10
 
 
 @pytest.mark.gpu
