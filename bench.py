@@ -15,7 +15,10 @@ CPU baseline, the same decode step with the per-head q/k norm, RoPE and KV store
 the attention launch (against the two-launch chain), the ragged causal prefill of 32 prompts of U[64, 2048] tokens
 (TFLOP/s against the dense bf16 MFMA peak) with its paged KV store (GB/s), and
 (unless --no-e2e) the end-to-end output tok/s of the 32 x 256-in / 2048-out
-greedy workload next to the reference's published 910B3 figure.
+greedy workload and of the 100 x 2048 / 2048 load workload (half the requests share
+a 1024-token prefix, prefix cache on, batch-100 decode graph; unless --no-load),
+each next to the reference's published 910B3 figure, with truncated runs of the
+fp32 CPU oracle model on the same weights beside them.
 """
 from __future__ import annotations
 
@@ -33,6 +36,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 REFERENCE_E2E_TOK_S = 1296.05  # nano_vllm_ascend on Ascend 910B3, 32 x 256/2048, bench_outputs/nano_32x256_2048.json
+REFERENCE_LOAD_TOK_S = 1410.23  # the same on 100 x 2048/2048 (batch-100 graph), bench_outputs/nano_100_2048_2048.json
 NUM_LAYERS = 28
 
 
@@ -45,10 +49,12 @@ def parse_args():
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work budget of the baseline sample")
     ap.add_argument("--e2e-prompts", type=int, default=32)
     ap.add_argument("--e2e-input", type=int, default=256)
     ap.add_argument("--e2e-output", type=int, default=2048)
+    ap.add_argument("--no-load", action="store_true",
+                    help="skip the 100 x 2048/2048 shared-prefix workload (prefix cache on, batch-100 graph)")
+    ap.add_argument("--load-output", type=int, default=2048)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run 5 device copies of MB megabytes (calibrates HBM byte counters), then exit")
     return ap.parse_args()
@@ -67,17 +73,41 @@ def copy_probe(mb: int) -> None:
     print(json.dumps({"copy_probe_bytes": n, "launches": 5}))
 
 
-def load_traffic(workload: str):
-    """HBM bytes per launch measured with rocprofv3 PMC counters (committed under profiles/), if present."""
+def kernel_source_sha(name: str) -> str:
+    import hashlib
+
+    return hashlib.sha256((ROOT / "nano_vllm_ascend_amd" / "csrc" / name).read_bytes()).hexdigest()[:16]
+
+
+def load_traffic(workload: str) -> tuple[float | None, str]:
+    """HBM bytes per launch from rocprofv3 PMC counters (FETCH_SIZE, WRITE_SIZE runs; committed under
+    profiles/traffic.json with the hash of the kernel source they were measured on) and where the
+    figure comes from.  A figure measured on another version of the source is stale: None."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
-        return None
+        return None, "no profiles/traffic.json"
     try:
-        data = json.loads(path.read_text())
-        entry = data.get(workload)
-        return None if entry is None else float(entry["bytes_per_launch"])
-    except Exception:
-        return None
+        entry = json.loads(path.read_text()).get(workload)
+    except ValueError:
+        return None, "profiles/traffic.json unreadable"
+    if entry is None:
+        return None, f"no entry for {workload} in profiles/traffic.json"
+    src = entry.get("kernel_source", "paged_decode.hip")
+    if entry.get("kernel_source_sha256") != kernel_source_sha(src):
+        return None, f"stale: profiles/traffic.json was measured on another version of csrc/{src}"
+    return float(entry["bytes_per_launch"]), (f"rocprofv3 PMC (FETCH_SIZE x{entry['fetch_scale']:g}, WRITE_SIZE "
+                                              f"x{entry['write_scale']:g}), {entry['source']}, csrc/{src} "
+                                              f"sha256 {entry['kernel_source_sha256']}")
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def decode_leg(args, device):
@@ -192,9 +222,13 @@ def fused_step_leg(args, work, device) -> dict:
 
     two = us_per_layer(two_launches)
     one = us_per_layer(fused)
+    # algorithmic bytes of the step: the attention's, plus raw q/k/v read, the new k/v stored
+    step_bytes = (sum(work.context_lens_list) * hkv * d * 2 * 2 + 2 * b * hq * d * 2 + b * work.block_tables.shape[1] * 4
+                  + b * 4 + b * ((hq + hkv) * d * 2 + hkv * d * 2 + 2 * hkv * d * 2 + 16))
     return {"workload": "decode step, 32 seqs, context U[256, 2304]: q/k norm + RoPE + KV store + attention",
             "two_launches_us_per_layer": round(two, 3), "fused_us_per_layer": round(one, 3),
-            "saved_us_per_layer": round(two - one, 3)}
+            "saved_us_per_layer": round(two - one, 3), "bytes": step_bytes,
+            "fused_gbs": round(step_bytes / one / 1e3, 1)}
 
 
 def small_decode_leg(args, device) -> dict:
@@ -411,11 +445,15 @@ def pack_leg(args, device) -> dict:
             "note": "wall time per call: host descriptors, one upload, pack kernel, synchronise"}
 
 
-def cpu_baseline(work, seconds: float):
-    """fp32 oracle on the host cores over a bounded sample: one layer's decode of the same batch, repeated."""
+def cpu_baseline(work, seed: int, reps: int = 20):
+    """fp32 oracle on the host cores: the 32-sequence decode step of one layer (layer 0 of the same
+    batch), whole -- per-head q/k RMSNorm + RoPE, the new token's K/V written into its page
+    (index_copy_ into the flattened cache, as PagedKVCache.write), paged decode attention -- and the
+    attention alone; medians of `reps` runs after 3 warm-ups."""
     import torch
 
-    from oracle.attention_ref import paged_decode_ref
+    from nano_vllm_ascend_amd import workloads as W
+    from oracle.attention_ref import paged_decode_ref, qk_norm_rope_ref
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -432,25 +470,53 @@ def cpu_baseline(work, seconds: float):
     for i in range(b):
         tables[i, : need[i]] = torch.arange(pos, pos + need[i], dtype=torch.int32)
         pos += need[i]
-    q = work.q.cpu()
+    inp = W.fused_step_inputs(work, seed, work.q.device)
+    qkv = inp.qkv.cpu()
+    q = qkv[:, : 16 * 128].view(b, 16, 128)
+    k = qkv[:, 16 * 128: 24 * 128].view(b, 8, 128)
+    v = qkv[:, 24 * 128:].view(b, 8, 128)
+    qw, kw, positions = inp.q_weight.cpu(), inp.k_weight.cpu(), inp.positions.cpu()
+    slots = torch.tensor([int(tables[i, p // bs]) * bs + p % bs for i, p in enumerate(positions.tolist())])
     ctx = work.context_lens.cpu()
     scale = 128 ** -0.5
-    paged_decode_ref(q, kc, vc, tables, ctx, scale)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        paged_decode_ref(q, kc, vc, tables, ctx, scale)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 200:
-            break
-    bytes_per = sum(work.context_lens_list) * 8 * 128 * 2 * 2 + 2 * b * 16 * 128 * 2 + b * bt.shape[1] * 4 + b * 4
+    kflat, vflat = kc.view(-1, 8, 128), vc.view(-1, 8, 128)
+
+    def step():
+        qn, kn = qk_norm_rope_ref(q, k, qw, kw, positions, W.ROPE_THETA, W.RMS_EPS, 4096)
+        kflat.index_copy_(0, slots, kn)
+        vflat.index_copy_(0, slots, v)
+        paged_decode_ref(qn, kc, vc, tables, ctx, scale)
+
+    def attention():
+        paged_decode_ref(work_q, kc, vc, tables, ctx, scale)
+
+    work_q = work.q.cpu()
+
+    def median(fn):
+        for _ in range(3):
+            fn()
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[reps // 2]
+
+    t_step, t_attn = median(step), median(attention)
+    attn_bytes = sum(work.context_lens_list) * 8 * 128 * 2 * 2 + 2 * b * 16 * 128 * 2 + b * bt.shape[1] * 4 + b * 4
+    step_bytes = attn_bytes + b * ((16 + 8) * 128 * 2 * 2 + 8 * 128 * 2 + 2 * 8 * 128 * 2 + 16)
     return {
-        "value": bytes_per * reps / el / 1e9,
+        "value": round(step_bytes / t_step / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"fp32 torch-CPU oracle, layer-0 decode of the same 32-sequence batch, {reps} reps in {el:.1f} s",
-        "cpu": platform.processor() or platform.machine(),
+        "sample": f"fp32 torch-CPU oracle, the decode step of layer 0 of the same 32-sequence batch (q/k norm + "
+                  f"RoPE + KV write + paged attention), median of {reps} after 3 warm-ups; GB/s of the step's "
+                  f"algorithmic bytes",
+        "step_ms": round(t_step * 1e3, 2),
+        "attention_only": {"ms": round(t_attn * 1e3, 2), "gbs": round(attn_bytes / t_attn / 1e9, 3),
+                           "note": "same bytes as the GPU value"},
+        "cpu": cpu_model(),
     }
 
 
@@ -512,6 +578,34 @@ def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 2) -> dict:
     }
 
 
+def cpu_e2e_truncated(state, config, prompts: list[list[int]], n_decode: int, workload: str) -> dict:
+    """fp32 oracle model on the host cores (oracle/qwen3_ref.py: one sequence at a time, dense cache,
+    the same weights) over a truncated run: each prompt's prefill, then `n_decode` greedy decode steps."""
+    import torch
+
+    from oracle.qwen3_ref import Qwen3Ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    ref = Qwen3Ref(state, config, round_bf16=True, max_positions=max(len(p) for p in prompts) + n_decode + 1)
+    t_prefill = t_decode = 0.0
+    for prompt in prompts:
+        ref.reset()
+        t0 = time.perf_counter()
+        tok = int(ref.forward(prompt).argmax())
+        t_prefill += time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for _ in range(n_decode):
+            tok = int(ref.forward([tok]).argmax())
+        t_decode += time.perf_counter() - t0
+    steps = len(prompts) * n_decode
+    return {"truncated": True, "kind": "port", "cores": cores, "cpu": cpu_model(),
+            "sample": f"{workload}: {len(prompts)} of its prompts, each prefilled then {n_decode} greedy decode steps, "
+                      f"one sequence at a time (fp32 CPU oracle model, same weights)",
+            "prefill_tok_s": round(sum(len(p) for p in prompts) / t_prefill, 2),
+            "decode_tok_s": round(steps / t_decode, 3), "decode_step_ms": round(t_decode / steps * 1e3, 1)}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -533,7 +627,7 @@ def main():
 
     dec = decode_leg(args, device)
     workload = "decode_b32_ctx256-2304_28layers"
-    traffic = load_traffic(workload)
+    traffic, traffic_source = load_traffic(workload)
     result = {
         "metric": "paged decode-attn HBM GB/s (% of peak); Qwen3-0.6B output tok/s 32x256/2048",
         "value": round(dec["value"], 2),
@@ -567,6 +661,7 @@ def main():
             "unit": "GB/s",
             "frac": round(dec["achieved"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "bytes_per_launch": dec["bytes_per_launch"],
             "avg_launch_us": round(dec["avg_launch_us"], 3),
             "median_launch_us": round(dec["median_launch_us"], 3),
@@ -577,7 +672,7 @@ def main():
     small = small_decode_leg(args, device)
     result["decode_small"] = {k: v for k, v in small.items() if k != "work"}
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(dec["work"], args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(dec["work"], args.seed)
         result["cpu_baseline_other"] = cpu_baselines_other(small["work"], args.seed)
     del dec, small
     torch.cuda.empty_cache()
@@ -590,9 +685,36 @@ def main():
         except ImportError:
             run_e2e = None
         if run_e2e is not None:
-            e2e = run_e2e(args.e2e_prompts, args.e2e_input, args.e2e_output, seed=args.seed, device=device)
+            from nano_vllm_ascend_amd import LLM
+            from nano_vllm_ascend_amd.bench_e2e import make_dataset
+            from nano_vllm_ascend_amd.config import QWEN3_0_6B
+
+            cfg = QWEN3_0_6B
+            need = args.e2e_prompts * -(-(args.e2e_input + args.e2e_output) // 128)
+            llm = LLM(cfg, max_model_len=4096, num_blocks=need + 64, max_num_seqs=args.e2e_prompts, seed=args.seed)
+            e2e = run_e2e(args.e2e_prompts, args.e2e_input, args.e2e_output, seed=args.seed, llm=llm)
             e2e["vs_reference_910B3"] = round(e2e["output_tok_s"] / REFERENCE_E2E_TOK_S, 3)
             result["e2e"] = e2e
+            state = None
+            if not args.no_cpu:
+                state = {k: v.detach().to("cpu") for k, v in llm.runner.model.state_dict().items()}
+            del llm
+            torch.cuda.empty_cache()
+            if not args.no_load:
+                load = run_e2e(100, 2048, args.load_output, seed=args.seed, shared_prefix=1024, shared_fraction=0.5,
+                               enable_prefix_cache=True, graph_sizes=[1, 2, 4, 8, 16, 32, 64, 100])
+                load["vs_reference_910B3"] = round(load["output_tok_s"] / REFERENCE_LOAD_TOK_S, 3)
+                load["reference_note"] = ("the reference's 100 x 2048/2048 run (1410.2 output tok/s, batch-100 graph) "
+                                          "used random prompts without a shared prefix")
+                result["e2e_load"] = load
+                torch.cuda.empty_cache()
+            if state is not None:
+                p3 = make_dataset(args.e2e_prompts, args.e2e_input, cfg.vocab_size, args.seed)[:2]
+                p4 = make_dataset(100, 2048, cfg.vocab_size, args.seed, shared_prefix=1024, shared_fraction=0.5)[:1]
+                result["cpu_baseline_e2e"] = {
+                    "32x256/2048": cpu_e2e_truncated(state, cfg, p3, 32, "32 x 256/2048"),
+                    "100x2048/2048": cpu_e2e_truncated(state, cfg, p4, 32, "100 x 2048/2048"),
+                }
     print(json.dumps(result))
 
 

@@ -260,7 +260,7 @@ int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
                       int vocab, int64_t *out, hipStream_t stream);
 
 /* ------------------------------------------------------------------------- */
-/* Skinny-M projections of the decode step (m <= 32 rows), a weight stream:   */
+/* Skinny-M projections of the decode step (m <= 128 rows), a weight stream:  */
 /*   acc[r, c] = sum_k a[r, k] * w[c, k] (fp32), for the decoder's qkv / o /  */
 /*   gate_up / down projections and the LM head at decode batch sizes        */
 /*   (F.linear at nv/models/qwen3.py:26-35, 48-51, 119 and                    */
@@ -291,7 +291,7 @@ int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
 /* y 8-byte aligned; row strides in elements (x: multiple of 8; y: of 4).     */
 /* Shapes that split K over workgroups need a zero-filled workspace of        */
 /* nvamd_skinny_linear_workspace_size(n, k, epilogue) bytes (0: none); calls  */
-/* leave it zero-filled and must not overlap.  m > 32: NVAMD_EUNSUPPORTED.   */
+/* leave it zero-filled and must not overlap.  m > 128: NVAMD_EUNSUPPORTED.  */
 /* embed_rows: out[r] = table[ids[r]] (zeros for an id outside [0, vocab)),   */
 /*   the token embedding (torch.embedding at nv/layers/embed_head.py:20-21),  */
 /*   and, if ssq != NULL, ssq[r * (hidden/32) + t] = sum of squares of        */

@@ -438,7 +438,7 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     return out
 
 
-SKINNY_MAX_ROWS = 32  # rows the skinny projection kernels take (decode batches)
+SKINNY_MAX_ROWS = 128  # rows the skinny projection kernels take (decode batches)
 EPI_STORE, EPI_SILU, EPI_RESID = 0, 1, 2
 
 
@@ -484,7 +484,7 @@ def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = N
                   x_ssq: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
                   y_ssq: torch.Tensor | None = None, workspace: torch.Tensor | None = None, m: int | None = None,
                   y_tiled: bool = False) -> torch.Tensor:
-    """Decode-batch projection x[M, K] @ W^T (M <= 32) with an optional RMSNorm prologue and a store,
+    """Decode-batch projection x[M, K] @ W^T (M <= 128) with an optional RMSNorm prologue and a store,
     SiLU*mul or residual-add epilogue (one HIP launch).  Returns the output (the residual for EPI_RESID).
 
     w is the weight tiled (``tile(W)``; SILU: the fused [2I, K] gate/up weight).  x is row-major
@@ -534,13 +534,13 @@ def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = N
 
 def linear(x: torch.Tensor, w_tiled: torch.Tensor, out: torch.Tensor | None = None,
            workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """x[M, K] @ W[N, K]^T in bf16 for M <= 32 (HIP skinny GEMM; w_tiled = tile(W))."""
+    """x[M, K] @ W[N, K]^T in bf16 for M <= 128 (HIP skinny GEMM; w_tiled = tile(W))."""
     return skinny_linear(x, w_tiled, out, workspace=workspace)
 
 
 def linear_silu_mul(x: torch.Tensor, w_gate_up_tiled: torch.Tensor, out: torch.Tensor | None = None,
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """silu(x @ W[:I]^T) * (x @ W[I:]^T) in bf16 for M <= 32 (one HIP launch; W the [2I, K] gate/up
+    """silu(x @ W[:I]^T) * (x @ W[I:]^T) in bf16 for M <= 128 (one HIP launch; W the [2I, K] gate/up
     weight, passed as tile(W))."""
     _require(w_gate_up_tiled.shape[0] % 2 == 0, "the gate/up weight must be [2I, K]")
     return skinny_linear(x, w_gate_up_tiled, out, epilogue=EPI_SILU, workspace=workspace)

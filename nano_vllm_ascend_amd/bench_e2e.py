@@ -14,10 +14,16 @@ seeded 1024-token prefix, prefix cache on (the reference's own run of 100 x
 2048 / 2048 is bench_outputs/nano_100_2048_2048.json) -- is
 
     python -m nano_vllm_ascend_amd.bench_e2e --prompts 100 --input 2048 --output 2048 \
-        --shared-prefix 1024 --shared-fraction 0.5 --prefix-cache
+        --shared-prefix 1024 --shared-fraction 0.5 --prefix-cache --graph-sizes 1,2,4,8,16,32,64,100
 
-With the prefix cache on, the warm-up uses a different seed and the cache is
-cleared before the timed run, so only the intended sharing can hit.
+With the prefix cache on, the warm-up uses a different seed and a short output,
+the cache is cleared, and then one seed request carrying the shared prefix is run
+(its prefill caches the prefix's full blocks), so in the timed run exactly the
+requests that share the prefix hit it.  The prefix lookup happens at submit time
+and blocks are cached only after their prefill (nv/model_runner.py:146-167,
+232-238), so without the seed request a run that submits everything before any
+prefill could not hit at all.  The result reports the hits.  ``--graph-sizes``
+sets the captured decode batch sizes (the load workload captures its batch of 100).
 """
 from __future__ import annotations
 
@@ -30,7 +36,6 @@ import torch
 
 from .config import QWEN3_0_6B
 from .engine import LLM
-from .sequence import Sequence
 
 
 def make_dataset(num_prompts: int, input_len: int, vocab_size: int, seed: int, token_id_high: int = 10000,
@@ -48,48 +53,44 @@ def make_dataset(num_prompts: int, input_len: int, vocab_size: int, seed: int, t
 
 
 def generate_from_token_ids(llm: LLM, prompts: list[list[int]], output_len: int, sampling_params=None):
-    """Submit token ids directly (no tokenizer), run to completion, return generated ids per request."""
-    from .sampling_params import SamplingParams
-
-    params = sampling_params or SamplingParams()
-    llm.scheduler.reset()
-    ids = []
-    for toks in prompts:
-        seq = Sequence(seq_id=llm.scheduler.next_seq_id(), prompt="", max_new_tokens=output_len,
-                       prompt_token_ids=torch.tensor(toks, dtype=torch.long), sampling_params=params)
-        llm.runner.prepare_sequences([seq])
-        seq.reserved_blocks = llm.scheduler.compute_required_blocks(runtime_prompt_len=seq.runtime_prompt_len,
-                                                                    max_new_tokens=output_len)
-        llm.scheduler.add_request(seq)
-        ids.append(seq.seq_id)
-    out = {}
-    while llm.has_unfinished():
-        for o in llm.step():
-            out[o["request_id"]] = o["token_ids"]
-    return [out.get(i, []) for i in ids]
+    """Run prompts given as token ids to completion (``LLM.generate``); generated ids per request."""
+    return [o["token_ids"] for o in llm.generate(prompts, max_new_tokens=output_len, sampling_params=sampling_params)]
 
 
 def run_e2e(num_prompts: int = 32, input_len: int = 256, output_len: int = 2048, seed: int = 0, device=None,
             max_model_len: int = 4096, block_size: int = 128, warmup: int = 1, num_blocks: int | None = None,
             enable_decode_graph: bool = True, llm: LLM | None = None, shared_prefix: int = 0,
-            shared_fraction: float = 0.0, enable_prefix_cache: bool = False) -> dict:
-    cfg = QWEN3_0_6B
+            shared_fraction: float = 0.0, enable_prefix_cache: bool = False,
+            graph_sizes: list[int] | None = None, config=None) -> dict:
+    cfg = config or QWEN3_0_6B
     need = num_prompts * -(-(input_len + output_len) // block_size)
     if llm is None:
         llm = LLM(cfg, max_model_len=max_model_len, block_size=block_size, num_blocks=num_blocks or need + 64,
                   max_num_seqs=num_prompts, enable_decode_graph=enable_decode_graph, seed=seed,
-                  enable_prefix_cache=enable_prefix_cache)
+                  enable_prefix_cache=enable_prefix_cache, decode_graph_batch_sizes=graph_sizes)
     llm.runner.tokenizer.eos_token_id = -1  # ignore EOS, as the reference benchmark does
     prompts = make_dataset(num_prompts, input_len, cfg.vocab_size, seed, shared_prefix=shared_prefix,
                            shared_fraction=shared_fraction)
     for w in range(warmup):
-        warm = prompts if not enable_prefix_cache else make_dataset(
-            num_prompts, input_len, cfg.vocab_size, seed + 1 + w, shared_prefix=shared_prefix,
-            shared_fraction=shared_fraction)
-        generate_from_token_ids(llm, warm, output_len)
+        if enable_prefix_cache:  # other prompts and a short output: graphs captured, nothing cached that hits
+            warm = make_dataset(num_prompts, input_len, cfg.vocab_size, seed + 1 + w, shared_prefix=shared_prefix,
+                                shared_fraction=shared_fraction)
+            generate_from_token_ids(llm, warm, min(output_len, 16))
+        else:
+            generate_from_token_ids(llm, prompts, output_len)
         torch.cuda.synchronize()
+    seeded = 0
     if enable_prefix_cache:
         llm.clear_prefix_cache()
+        if shared_prefix and shared_fraction:
+            # one seed request carrying the shared prefix caches its full blocks
+            n_shared = round(shared_fraction * num_prompts)
+            seed_prompt = prompts[0][: shared_prefix] + [prompts[n_shared % num_prompts][0]]
+            generate_from_token_ids(llm, [seed_prompt], 1)
+            seeded = shared_prefix // block_size
+        torch.cuda.synchronize()
+    graph0 = dict(llm.runner.decode_graph_stats())
+    prefill0 = dict(llm.runner.prefill_stats)
     t0 = time.perf_counter()
     outs = generate_from_token_ids(llm, prompts, output_len)
     torch.cuda.synchronize()
@@ -99,15 +100,25 @@ def run_e2e(num_prompts: int = 32, input_len: int = 256, output_len: int = 2048,
     if shared_prefix and shared_fraction:
         workload += f", {shared_fraction:g} of requests share a {shared_prefix}-token prefix"
     if enable_prefix_cache:
-        workload += ", prefix cache on"
+        workload += ", prefix cache on" + (", warmed by one seed request carrying the prefix" if seeded else "")
+    seqs = list(llm.scheduler.finished.values())
+    hits = [s for s in seqs if s.cached_prefix_len > 0]
+    graph = {k: v - graph0.get(k, 0) for k, v in llm.runner.decode_graph_stats().items()}
+    prefill = {k: v - prefill0.get(k, 0) for k, v in llm.runner.prefill_stats.items()}
     return {
         "workload": workload,
         "output_tok_s": round(generated / elapsed, 2),
         "total_tok_s": round((generated + num_prompts * input_len) / elapsed, 2),
         "elapsed_s": round(elapsed, 3),
         "generated_tokens": generated,
-        "decode_graph": llm.runner.decode_graph_stats(),
+        "decode_graph": llm.runner.decode_graph_stats(),  # the whole run, warm-up included
+        "decode_graph_timed": graph,
+        "decode_graph_batch_sizes": sorted(llm.runner.decode_graph_runner.batch_sizes)
+        if llm.runner.decode_graph_runner is not None else [],
         "overlapped_steps": dict(llm.runner.overlap_stats),
+        "prefix_cache": {"requests_with_hits": len(hits), "hit_blocks": sum(len(s.cached_block_ids) for s in hits),
+                         "hit_tokens": sum(s.cached_prefix_len for s in hits), "prefill": prefill}
+        if enable_prefix_cache else None,
         "model": "Qwen3-0.6B shape, seeded N(0, 0.02) weights, bf16",
     }
 
@@ -124,11 +135,14 @@ def main():
     ap.add_argument("--shared-fraction", type=float, default=0.0, help="fraction of requests that share it")
     ap.add_argument("--prefix-cache", action="store_true")
     ap.add_argument("--max-model-len", type=int, default=4096)
+    ap.add_argument("--graph-sizes", type=str, default=None,
+                    help="comma-separated captured decode batch sizes (default: 1,2,4,8,16,32)")
     args = ap.parse_args()
+    sizes = [int(x) for x in args.graph_sizes.split(",")] if args.graph_sizes else None
     print(json.dumps(run_e2e(args.prompts, args.input, args.output, args.seed, warmup=args.warmup,
                              enable_decode_graph=not args.no_graph, shared_prefix=args.shared_prefix,
                              shared_fraction=args.shared_fraction, enable_prefix_cache=args.prefix_cache,
-                             max_model_len=args.max_model_len)))
+                             max_model_len=args.max_model_len, graph_sizes=sizes)))
 
 
 if __name__ == "__main__":

@@ -1,4 +1,4 @@
-// Skinny-M projections of the decode step (M <= 32 rows): Y[M, N] = X[M, K] . W[N, K]^T
+// Skinny-M projections of the decode step (M <= 128 rows): Y[M, N] = X[M, K] . W[N, K]^T
 // for the per-layer qkv / o / gate_up / down projections and the LM head
 // (F.linear at nv/models/qwen3.py:26-35, 48-51, 119; nv/layers/embed_head.py:24-39),
 // with the decoder's residual-add + RMSNorm folded into the GEMMs on either side of it
@@ -16,10 +16,12 @@
 //     M = 32 projections (inside the decode step: qkv 7.0 -> 6.1 us, gate/up 8.3 -> 7.3 us).
 //     Row-major X rows past M repeat row M-1;
 //     a tiled X holds 16 * ceil(M/16) rows, and rows past M only reach dropped outputs;
-//   * a workgroup of NW waves owns 16*NT output columns and one of KS slices of K
+//   * a workgroup of NW waves owns 16*NT output columns, one of KS slices of K
 //     (split-K across workgroups where the column count alone gives too few
-//     workgroups); its waves split the slice again, and a wave's NT column tiles share
-//     each A fragment;
+//     workgroups) and one 32-row slab of X (M > 32: ceil(M/32) slabs, the slab index
+//     fastest in the grid, so the slabs reading one weight tile run side by side and
+//     its repeat reads come from the Infinity Cache); its waves split the slice again,
+//     and a wave's NT column tiles share each A fragment;
 //   * the waves' partial tiles meet in LDS; with KS > 1 the workgroups publish fp32
 //     partials with agent-scope write-through stores, count arrivals per column group,
 //     and the last to arrive adds the KS partials in slice order.  Every sum has a
@@ -110,9 +112,27 @@ skinny_gemm_kernel(GemmArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  const int group = blockIdx.x / a.ks;
-  const int slice = blockIdx.x - group * a.ks;
+  // Grid: (column group, K slice, 32-row slab), slab fastest.  The slab's rows become rows
+  // 0..31 of this workgroup: operand, norm-partial and output pointers move to its first row,
+  // and its split-K partials and counters follow those of the earlier slabs.
+  const int slabs = (a.m + 31) >> 5;
+  const int slab = blockIdx.x % slabs;
+  const int gs = blockIdx.x / slabs;
+  const int group = gs / a.ks;
+  const int slice = gs - group * a.ks;
   const int n0 = group * CW;
+  if (slab > 0) {
+    const int64_t r0 = 32 * (int64_t)slab;
+    a.x += a.x_tiled ? 2 * slab * (int64_t)(a.k >> 5) * 512 : r0 * a.x_stride;
+    if (NORM) a.x_ssq += r0 * (a.k >> 5);
+    a.y += a.y_tiled ? 2 * slab * (int64_t)(a.n >> 5) * 512 : r0 * a.y_stride;
+    if (EPI == kEpiResid) a.y_ssq += r0 * (a.n >> 5);
+    const int groups = gridDim.x / (slabs * a.ks);
+    a.counters += slab * groups;
+    a.partials += (int64_t)slab * groups * a.ks * NACC * TF;
+    a.m -= 32 * slab;
+  }
+  a.m = min(a.m, 32);
 
   // Operand addresses: base + k0 * step for the 32-wide K step starting at k0 (tiled: the
   // step's 512-element tile follows the previous one, so 16 elements per unit of k).
@@ -122,7 +142,10 @@ skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     xr[mt] = min(16 * mt + n, a.m - 1);
-    xp[mt] = a.x_tiled ? a.x + (int64_t)mt * (a.k >> 5) * 512 + 8 * lane : a.x + (int64_t)xr[mt] * a.x_stride + 8 * g;
+    // a tiled X holds 16 * ceil(M/16) rows: an M tile past the slab's last row re-reads its last
+    // tile (those rows only reach dropped outputs)
+    const int mt_x = min(mt, (a.m - 1) >> 4);
+    xp[mt] = a.x_tiled ? a.x + (int64_t)mt_x * (a.k >> 5) * 512 + 8 * lane : a.x + (int64_t)xr[mt] * a.x_stride + 8 * g;
   }
   const u16 *wp[NACC];
 #pragma unroll
@@ -320,11 +343,13 @@ Plan make_plan(int n, int k, int epi) {
   return p;
 }
 
+constexpr int kMaxSlabs = 4;  // M <= 128
+
 size_t workspace_bytes_for(const Plan &p, int n, int epi) {
   if (p.ks <= 1) return 0;
   const int nacc = (epi == kEpiSilu ? 2 : 1) * p.nt;
   const size_t groups = (size_t)n / (16 * p.nt);
-  return kCounterBytes + groups * p.ks * nacc * 32 * 16 * sizeof(float);
+  return kCounterBytes + kMaxSlabs * groups * p.ks * nacc * 32 * 16 * sizeof(float);
 }
 
 template <int NW, int KB, int NT, int EPI, bool NORM>
@@ -373,7 +398,7 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
   if (!x || !w_tiled || !y || m < 0 || n <= 0 || k <= 0 || epilogue < 0 || epilogue > 2 ||
       (flags & ~(NVAMD_GEMM_X_TILED | NVAMD_GEMM_Y_TILED)))
     return NVAMD_EINVAL;
-  if (m > 32 || n % 32 != 0 || k % 256 != 0) return NVAMD_EUNSUPPORTED;
+  if (m > 32 * kMaxSlabs || n % 32 != 0 || k % 256 != 0) return NVAMD_EUNSUPPORTED;
   const bool x_tiled = flags & NVAMD_GEMM_X_TILED, y_tiled = flags & NVAMD_GEMM_Y_TILED;
   const bool norm = x_ssq != nullptr;
   if (norm && !norm_weight) return NVAMD_EINVAL;
@@ -386,8 +411,9 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
   const Plan p = make_plan(n, k, epilogue);
   const int groups = n / (16 * p.nt);
   if ((k / p.ks) % (32 * p.kb) != 0) return NVAMD_EUNSUPPORTED;  // whole wave blocks per slice
+  const int slabs = (m + 31) / 32;
   if (p.ks > 1) {
-    if (groups > kCounterSlots) return NVAMD_EUNSUPPORTED;
+    if (groups * slabs > kCounterSlots) return NVAMD_EUNSUPPORTED;
     if (!workspace || !aligned16(workspace) || workspace_bytes < workspace_bytes_for(p, n, epilogue))
       return NVAMD_EWORKSPACE;
   }
@@ -410,7 +436,7 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
   a.k_slice = k / p.ks;
   a.counters = static_cast<int *>(workspace);
   a.partials = workspace ? reinterpret_cast<float *>(static_cast<char *>(workspace) + kCounterBytes) : nullptr;
-  const int grid = groups * p.ks;
+  const int grid = groups * p.ks * slabs;
   switch (epilogue) {
     case kEpiSilu:
       return norm ? dispatch<kEpiSilu, true>(a, p, grid, stream) : dispatch<kEpiSilu, false>(a, p, grid, stream);

@@ -143,6 +143,9 @@ class ModelRunner:
         self._fetch: dict[int, list] = {}      # batch size -> [two _TokenFetch, next index]
         self._logits_keep: dict[int, torch.Tensor] = {}
         self.overlap_stats = {"launched": 0, "used": 0, "discarded": 0}
+        # prefill batches, those on the paged (prefix-hit) route, and the prompt tokens whose K/V
+        # came from the prefix cache instead of being computed
+        self.prefill_stats = {"batches": 0, "paged_batches": 0, "cached_tokens": 0, "computed_tokens": 0}
         # test hook: called as hook(kind, slots, metadata) with a host copy of the metadata of
         # every prefill and every decode step that is actually taken
         self.metadata_hook = None
@@ -256,6 +259,11 @@ class ModelRunner:
             start_positions=[s.cached_prefix_len for s in seqs], prefix_block_ids=[s.cached_block_ids for s in seqs],
             token_ids=[np.asarray(s.runtime_prompt_token_ids) for s in seqs])
         self._report("prefill", [s.seq_id for s in seqs], md)
+        st = self.prefill_stats
+        st["batches"] += 1
+        st["paged_batches"] += int(md.use_paged_prefill)
+        st["cached_tokens"] += sum(s.cached_prefix_len for s in seqs)
+        st["computed_tokens"] += sum(s.runtime_prompt_len for s in seqs)
         out = self.model(input_ids_flat=md.input_ids, position_ids_flat=md.positions, kv_cache=self.kv_cache,
                          attn_metadata=md, is_prefill=True, logits_indices=md.last_token_indices)
         self.last_logits = out.logits  # rows in `seqs` order; a graph replay reuses this buffer

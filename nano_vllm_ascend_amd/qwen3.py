@@ -8,7 +8,7 @@ batch runs all of it inside the paged-decode launch (one kernel, identical bits)
 are views into the fused projection output, which the kernels accept through their row
 strides.
 
-Decode batches of <= 32 rows take a fused path (``forward_decode_fused``): the
+Decode batches of <= 128 rows take a fused path (``forward_decode_fused``): the
 skinny-M HIP GEMM runs every projection, each RMSNorm in the prologue of the GEMM
 that consumes it, and each residual add in the epilogue of the GEMM that produces
 it (with the per-32-column sums of squares the next norm needs), and SiLU*mul in
@@ -89,7 +89,7 @@ class Qwen3Attention(nn.Module):
     def decode_fused(self, residual, ssq, t: int, norm: RMSNorm, rotary, positions, kv_cache, attn_metadata,
                      workspace):
         """residual += o_proj(attention(qkv_proj(norm(residual)))) in place, for a decode batch of
-        t <= 32 rows held tiled in `residual`: the input RMSNorm runs in the qkv GEMM's prologue and
+        t <= 128 rows held tiled in `residual`: the input RMSNorm runs in the qkv GEMM's prologue and
         the residual add (with the sums of squares the next norm needs) in the o_proj GEMM's epilogue."""
         qkv = _C.skinny_linear(residual, self.qkv_tiled, x_ssq=ssq, norm_weight=norm.weight,
                                eps=norm.variance_epsilon, workspace=workspace, m=t)
@@ -118,7 +118,7 @@ class Qwen3MLP(nn.Module):
         return linear(gate_up_silu(x, self.gate_up_weight, self.gate_up_tiled), self.down_weight, skinny=False)
 
     def decode_fused(self, residual, ssq, t: int, norm: RMSNorm, workspace):
-        """residual += down(silu(gate(norm(residual))) * up(norm(residual))) in place (t <= 32 rows,
+        """residual += down(silu(gate(norm(residual))) * up(norm(residual))) in place (t <= 128 rows,
         tiled): norm in the gate/up GEMM's prologue, SiLU*mul in its epilogue (written tiled), the
         residual add in the down GEMM's epilogue."""
         act = _C.skinny_linear(residual, self.gate_up_tiled, epilogue=_C.EPI_SILU, x_ssq=ssq,
@@ -165,7 +165,7 @@ class Qwen3Model(nn.Module):
         return x
 
     def forward_decode_fused(self, input_ids_flat, position_ids_flat, kv_cache, attn_metadata, workspace):
-        """Decode forward for <= 32 rows with every RMSNorm and residual add folded into the
+        """Decode forward for <= 128 rows with every RMSNorm and residual add folded into the
         projections: 5 launches per layer (qkv, norm/RoPE/store + attention, o, gate_up, down).
         Returns the final residual stream (tiled, 16 * ceil(t/16) rows) and its per-32-column sums
         of squares; the final norm runs in the LM head's prologue."""

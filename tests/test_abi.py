@@ -90,7 +90,7 @@ def test_skinny_linear_argument_errors():
         return lib.nvamd_skinny_linear(*args.values())
 
     assert call(m=0) == 0
-    assert call(m=33) == EUNSUPPORTED                      # at most 32 rows
+    assert call(m=129) == EUNSUPPORTED                     # at most 128 rows
     assert call(flags=4) == EINVAL                         # unknown flag
     assert call(x_stride=1000) == EINVAL                   # row-major x rows shorter than k
     assert call(w=A + 8) == EINVAL                         # the tiled weight is read 16 bytes at a time

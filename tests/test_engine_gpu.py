@@ -184,37 +184,46 @@ def test_full_depth_greedy_tokens_against_oracle(device):
 
 
 @pytest.mark.gpu
-def test_fused_decode_path_matches_unfused_chain(device):
-    """Decode batches <= 32 rows fold every RMSNorm and residual add into the projections; the
-    logits must match the unfused chain (library GEMMs + add_rms_norm) of the same model to
-    rounding, and tokens may differ only at near-ties."""
-    fused, plain = make_llm(graph=False), make_llm(graph=False)
+@pytest.mark.parametrize("n_prompts", [4, 100])
+def test_fused_decode_path_matches_unfused_chain(device, n_prompts):
+    """Decode batches <= 128 rows fold every RMSNorm and residual add into the projections (at
+    100 rows: four 32-row slabs per projection); the logits must match the unfused chain
+    (library GEMMs + add_rms_norm) of the same model to rounding, and tokens may differ only at
+    near-ties."""
+    kw = dict(graph=False) if n_prompts <= 8 else dict(graph=False, max_num_seqs=n_prompts, num_blocks=n_prompts * 3)
+    fused, plain = make_llm(**kw), make_llm(**kw)
     plain.runner.model.decode_fusable = lambda rows: False
-    prompts = prompts_for([37, 128, 200, 5], seed=3)
+    lens = [37, 128, 200, 5] if n_prompts == 4 else [random.Random(i).randint(5, 250) for i in range(n_prompts)]
+    prompts = prompts_for(lens, seed=3)
     for llm in (fused, plain):
         llm.runner.tokenizer.eos_token_id = -1
         for p in prompts:
             llm.submit(p, max_new_tokens=17)
-    worst, steps = 0.0, 0
+    # Rows are independent (attention per sequence, GEMM rows), so a row whose token differs at a
+    # near-tie leaves the comparison and the others go on.
+    worst, steps, live, dropped = 0.0, 0, set(range(n_prompts)), 0
     while fused.has_unfinished():
         fused.step()
         plain.step()
-        if steps > 0:  # the first step is the (shared, unfused) prefill
-            la, lb = fused.runner.last_logits.float(), plain.runner.last_logits.float()
-            assert la.shape == lb.shape
-            worst = max(worst, (la - lb).abs().max().item())
+        if not fused.has_unfinished():
+            break  # the last step only commits final tokens
+        la, lb = fused.runner.last_logits.float(), plain.runner.last_logits.float()
+        assert la.shape == lb.shape == (n_prompts, la.shape[1])
+        rows = sorted(live)
+        if steps > 0 and rows:  # the first step is the (shared, unfused) prefill
+            worst = max(worst, (la[rows] - lb[rows]).abs().max().item())
         steps += 1
         ta = [s.next_token_id for s in fused.scheduler.seqs.values()]
         tb = [s.next_token_id for s in plain.scheduler.seqs.values()]
-        if ta != tb:  # inputs diverge from here on: the differing token must be a near-tie
-            lb = plain.runner.last_logits.float()
-            for row, (x, y) in enumerate(zip(ta, tb)):
-                if x != y:
-                    assert (lb[row, y] - lb[row, x]).item() < TIE_TOL
-            break
-    print(f"fused vs unfused decode: {steps} steps compared, worst logit diff {worst:.4f}")
+        for row in rows:
+            if ta[row] != tb[row]:
+                assert (lb[row, tb[row]] - lb[row, ta[row]]).item() < TIE_TOL
+                live.discard(row)
+                dropped += 1
+    print(f"fused vs unfused decode at {n_prompts} rows: {steps} steps, worst logit diff {worst:.4f}, "
+          f"{dropped} rows left at near-ties")
     assert fused.runner.model._gemm_workspace is not None and plain.runner.model._gemm_workspace is None
-    assert steps >= 4 and worst <= 0.05
+    assert steps >= 16 and worst <= 0.05 and len(live) >= n_prompts // 2
 
 
 @pytest.mark.gpu

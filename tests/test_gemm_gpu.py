@@ -34,7 +34,7 @@ def _assert_close_bf16(y, ref, rel=ULP, slack=1e-5):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 7, 32])
+@pytest.mark.parametrize("m", [1, 7, 32, 33, 100, 128])
 @pytest.mark.parametrize("nk", SHAPES, ids=[f"n{n}_k{k}" for n, k in SHAPES])
 def test_linear_matches_fp32(device, m, nk):
     n, k = nk
@@ -55,7 +55,7 @@ def _bf16_steps(x, steps):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 5, 32])
+@pytest.mark.parametrize("m", [1, 5, 32, 77])
 def test_linear_silu_mul_matches_unfused_rounding(device, m):
     """Exact check: y = bf16(bf16(silu(g)) * u) for g, u the bf16 gate and up projections.
     A different fp32 summation order may round g or u to the neighbouring bf16 value (and an
@@ -110,8 +110,8 @@ def test_linear_is_deterministic(device):
 
 
 @pytest.mark.gpu
-def test_linear_rejects_more_than_32_rows(device):
-    x, w = _operands(33, 1024, 1024, device, seed=9)
+def test_linear_rejects_more_than_128_rows(device):
+    x, w = _operands(129, 1024, 1024, device, seed=9)
     with pytest.raises(ValueError):
         _C.linear(x, _C.tile(w))
 
@@ -130,7 +130,7 @@ def _tile_ssq(x):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 13, 32])
+@pytest.mark.parametrize("m", [1, 13, 32, 100])
 @pytest.mark.parametrize("nk", [(4096, 1024), (151936, 1024)], ids=["qkv", "lm_head"])
 def test_norm_prologue_matches_add_rms_norm_then_linear(device, m, nk):
     n, k = nk
@@ -157,7 +157,7 @@ def test_norm_prologue_matches_add_rms_norm_then_linear(device, m, nk):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 32])
+@pytest.mark.parametrize("m", [1, 32, 100])
 @pytest.mark.parametrize("nk", [(1024, 2048), (1024, 3072), (1024, 1024), (2048, 4096), (4096, 1024)],
                          ids=["o_proj", "down_proj", "split4_k1024", "split2_k4096", "unsplit_n4096"])
 def test_residual_epilogue(device, m, nk):
@@ -208,8 +208,9 @@ def test_split_k_is_deterministic_and_leaves_workspace_zero(device):
     outs = []
     for rep in range(3):
         for k in (2048, 3072):
-            x, w = _operands(32, 1024, k, device, seed=k)
-            outs.append((rep, k, _C.linear(x, _C.tile(w), workspace=ws)))
+            x, w = _operands(100, 1024, k, device, seed=k)
+            m = 100 if rep == 1 else 32  # rows are independent: the first 32 of 100 equal a 32-row call
+            outs.append((rep, k, _C.linear(x[:m], _C.tile(w), workspace=ws)[:32]))
     torch.cuda.synchronize()
     by_k = {}
     for rep, k, y in outs:
@@ -220,9 +221,10 @@ def test_split_k_is_deterministic_and_leaves_workspace_zero(device):
 
 
 @pytest.mark.gpu
-def test_graph_replays_equal_eager(device):
+@pytest.mark.parametrize("m", [32, 100])
+def test_graph_replays_equal_eager(device, m):
     """A captured decode-style chain (norm prologue, SiLU, residual) replays to the eager result."""
-    m, h, inter = 32, 1024, 3072
+    h, inter = 1024, 3072
     gen = torch.Generator(device=device).manual_seed(8)
     w_gu = _C.tile((torch.randn((2 * inter, h), generator=gen, device=device) * 0.02).to(torch.bfloat16))
     w_dn = _C.tile((torch.randn((h, inter), generator=gen, device=device) * 0.02).to(torch.bfloat16))
@@ -262,7 +264,7 @@ def test_graph_replays_equal_eager(device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 13, 17, 32])
+@pytest.mark.parametrize("m", [1, 13, 17, 32, 49, 100, 128])
 @pytest.mark.parametrize("epi", [_C.EPI_STORE, _C.EPI_SILU, _C.EPI_RESID], ids=["store", "silu", "resid"])
 def test_tiled_activations_equal_row_major(device, m, epi):
     """The same projection with x and y tiled gives the row-major results bit for bit (the same
