@@ -149,6 +149,61 @@ def version() -> int:
     return int(load().nvamd_version())
 
 
+# ------------------------------------------------------------------ optional host-side range checks
+# The kernels never read or write outside their buffers, but where the reference's torch indexing
+# (index_select of the RoPE cache, index_copy_ into the KV cache, the block-table gather) would
+# raise on an index out of range they clamp, skip or truncate instead.  With range checks on
+# (set_range_checks(True), or NVAMD_CHECK_RANGES=1 in the environment) the eager wrappers read the
+# indices back to the host and raise IndexError first.  That costs a device-to-host copy per call,
+# so it is a debugging aid, off by default; calls made while a graph is being captured are not
+# checked (a capture cannot synchronise).
+_range_checks = os.environ.get("NVAMD_CHECK_RANGES", "") not in ("", "0")
+
+
+def set_range_checks(enabled: bool) -> bool:
+    """Turn the host-side range checks on or off; returns the previous setting."""
+    global _range_checks
+    prev, _range_checks = _range_checks, bool(enabled)
+    return prev
+
+
+def _checking() -> bool:
+    return _range_checks and not (torch.cuda.is_available() and torch.cuda.is_current_stream_capturing())
+
+
+def check_positions(positions: torch.Tensor, max_positions: int) -> None:
+    """RoPE rows are index_select-ed by position (nv/layers/rotary_embedding.py:44-55)."""
+    pos = positions.detach().reshape(-1).cpu()
+    if pos.numel() and (int(pos.min()) < 0 or int(pos.max()) >= max_positions):
+        raise IndexError(f"position out of range [0, {max_positions}) of the RoPE table: "
+                         f"min {int(pos.min())}, max {int(pos.max())}")
+
+
+def check_slots(slot_mapping: torch.Tensor, num_slots: int) -> None:
+    """K/V rows are index_copy_-ed at their slots (nv/npu/paged_kv_cache.py:68-69); -1 marks a padding
+    row that is not stored (an extension the reference never emits)."""
+    sl = slot_mapping.detach().reshape(-1).cpu()
+    if sl.numel() and (int(sl.min()) < -1 or int(sl.max()) >= num_slots):
+        raise IndexError(f"slot out of range [0, {num_slots}) (or -1 for padding): "
+                         f"min {int(sl.min())}, max {int(sl.max())}")
+
+
+def check_paged_context(block_tables: torch.Tensor, context_lens: torch.Tensor, num_blocks: int, block_size: int,
+                        max_context_len: int | None = None) -> None:
+    """Every context fits its bound and its block-table row, and the entries it reads name pool blocks
+    (the reference gathers K/V through the table, nv/layers/npu_paged_attention.py:89-99)."""
+    ctx = context_lens.detach().reshape(-1).cpu().long()
+    bt = block_tables.detach().cpu().long()
+    width = bt.shape[1] * block_size
+    for i, c in enumerate(ctx.tolist()):
+        if c < 0 or c > width or (max_context_len is not None and c > max_context_len):
+            raise IndexError(f"context length {c} of row {i} is outside [0, min({width}, "
+                             f"{max_context_len if max_context_len is not None else width})]")
+        used = bt[i, : -(-c // block_size)]
+        if used.numel() and (int(used.min()) < 0 or int(used.max()) >= num_blocks):
+            raise IndexError(f"block-table row {i} names a block outside [0, {num_blocks}): {used.tolist()}")
+
+
 def paged_decode_workspace_size(max_batch: int, num_heads: int, num_kv_heads: int, max_context_len: int) -> int:
     return int(load().nvamd_paged_decode_workspace_size(max_batch, num_heads, num_kv_heads, max_context_len))
 
@@ -210,6 +265,8 @@ def _decode_args(out, q, key_cache, value_cache, block_tables, context_lens, sca
     _require(context_lens.dtype == torch.int32 and context_lens.numel() == b and context_lens.is_cuda,
              "context_lens must be int32 [B] on the device")
     _require(context_lens.is_contiguous(), "context_lens must be contiguous")
+    if _checking():
+        check_paged_context(block_tables, context_lens, nb, bs, int(max_context_len))
     return (out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), key_cache.data_ptr(),
             value_cache.data_ptr(), nb, bs, block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
             context_lens.data_ptr(), b, hq, hkv, d, float(scale), int(max_context_len))
@@ -251,6 +308,10 @@ def paged_decode_fused(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: t
     _require(block_tables.stride(1) == 1, "block_tables rows must be dense")
     _require(context_lens.dtype == torch.int32 and context_lens.numel() == b and context_lens.is_cuda
              and context_lens.is_contiguous(), "context_lens must be int32 [B] on the device")
+    if _checking():
+        check_paged_context(block_tables, context_lens, nb, bs, int(max_context_len))
+        check_positions(positions, cos_sin.shape[0])
+        check_slots(slot_mapping, nb * bs)
     status = lib.nvamd_paged_decode_fused(
         out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), k.data_ptr(), _row_stride(k),
         v.data_ptr(), _row_stride(v), q_weight.data_ptr(), k_weight.data_ptr(), positions.contiguous().data_ptr(),
@@ -276,6 +337,8 @@ def kv_cache_write(key_states: torch.Tensor, value_states: torch.Tensor, key_cac
     _require(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t and slot_mapping.is_cuda,
              f"slot_mapping numel {slot_mapping.numel()} != total_tokens {t}")
     num_slots = key_cache.numel() // (hkv * d)
+    if _checking():
+        check_slots(slot_mapping, num_slots)
     status = lib.nvamd_kv_cache_write(
         key_states.data_ptr(), _row_stride(key_states), value_states.data_ptr(), _row_stride(value_states),
         key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.contiguous().data_ptr(), t, hkv, d, num_slots,
@@ -311,6 +374,10 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_wei
         _require(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
         _require(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t, "slot_mapping must be int64 [T]")
         num_slots = key_cache.numel() // (hkv * d)
+    if _checking():
+        check_positions(positions, cos_sin.shape[0])
+        if store:
+            check_slots(slot_mapping, num_slots)
     status = lib.nvamd_qk_norm_rope(
         q.data_ptr(), _row_stride(q), k.data_ptr(), _row_stride(k), _ptr(v), _row_stride(v) if store else 0,
         q_weight.data_ptr(), k_weight.data_ptr(), positions.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0],
@@ -386,6 +453,8 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, v
     nb, bs, hkv, d = key_cache.shape
     n_seqs = cu_seqlens_q.numel() - 1
     _require(kv_lens.numel() >= n_seqs and block_tables.shape[0] >= n_seqs, "per-sequence metadata too short")
+    if _checking():
+        check_paged_context(block_tables[:n_seqs], kv_lens[:n_seqs], nb, bs)
     status = lib.nvamd_paged_prefill(
         out.data_ptr(), _row_stride(out), q.data_ptr(), _row_stride(q), key_cache.data_ptr(), value_cache.data_ptr(),
         nb, bs, block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1], cu_seqlens_q.data_ptr(),

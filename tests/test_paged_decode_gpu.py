@@ -194,3 +194,34 @@ def test_decode_graph_replays_read_device_context_lens(device):
         eager = run_decode(q, kc, vc, bt, cl, 4096, ws=ws)
         torch.cuda.synchronize()
         assert torch.equal(eager, out), f"replay {rep} differs from eager"
+
+
+@pytest.mark.gpu
+def test_range_checks_raise_before_launching(device):
+    """With range checks on, indices the reference's indexing would reject raise IndexError from the
+    eager wrappers (nothing is launched); in-range calls run as usual."""
+    from nano_vllm_ascend_amd.layers import RotaryEmbedding
+
+    work = W.make_decode(4, 1, 512, 64, seed=6, device=device)
+    q, kc, vc = work.q, work.key_cache[0], work.value_cache[0]
+    ws = _C.alloc_paged_decode_workspace(4, 16, 8, 512, device)
+    out = torch.zeros_like(q)
+    prev = _C.set_range_checks(True)
+    try:
+        _C.paged_decode(out, q, kc, vc, work.block_tables, work.context_lens, 128 ** -0.5, 512, ws)
+        too_long = work.context_lens.clone()
+        too_long[0] = work.block_tables.shape[1] * 128 + 1
+        with pytest.raises(IndexError):
+            _C.paged_decode(out, q, kc, vc, work.block_tables, too_long, 128 ** -0.5, 4096, ws)
+        k = torch.randn(2, 8, 128, device=device).bfloat16()
+        with pytest.raises(IndexError):
+            _C.kv_cache_write(k, k, kc, vc, torch.tensor([0, kc.shape[0] * 128], device=device))
+        table = RotaryEmbedding(128, 1024, 1e6).cos_sin.to(device)
+        qq = torch.randn(2, 16, 128, device=device).bfloat16()
+        with pytest.raises(IndexError):
+            _C.qk_norm_rope(qq, k.clone(), torch.ones(128, device=device).bfloat16(),
+                            torch.ones(128, device=device).bfloat16(), torch.tensor([3, 1024], device=device), table,
+                            1e-6)
+    finally:
+        _C.set_range_checks(prev)
+    torch.cuda.synchronize()
