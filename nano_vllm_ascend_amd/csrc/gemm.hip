@@ -96,7 +96,7 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[NACC][MT], const u32x4 (&
                                                           __builtin_bit_cast(bf16x8v, wv[t]), acc[t][mt], 0, 0, 0);
 }
 
-template <int NW, int KB, int NT, int MT, int EPI, bool NORM>
+template <int NW, int KB, int NT, int MT, int EPI, bool NORM, bool SLABS>
 __global__ void __launch_bounds__(NW * 64)
 skinny_gemm_kernel(GemmArgs a) {
   constexpr int kNW = NW;
@@ -112,16 +112,16 @@ skinny_gemm_kernel(GemmArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  // Grid: (column group, K slice, 32-row slab), slab fastest.  The slab's rows become rows
-  // 0..31 of this workgroup: operand, norm-partial and output pointers move to its first row,
-  // and its split-K partials and counters follow those of the earlier slabs.
-  const int slabs = (a.m + 31) >> 5;
-  const int slab = blockIdx.x % slabs;
-  const int gs = blockIdx.x / slabs;
+  // Grid: (column group, K slice[, 32-row slab]), slab fastest (SLABS: M > 32).  A slab's rows
+  // become rows 0..31 of this workgroup: operand, norm-partial and output pointers move to its
+  // first row, and its split-K partials and counters follow those of the earlier slabs.
+  const int slabs = SLABS ? (a.m + 31) >> 5 : 1;
+  const int slab = SLABS ? blockIdx.x % slabs : 0;
+  const int gs = SLABS ? blockIdx.x / slabs : blockIdx.x;
   const int group = gs / a.ks;
   const int slice = gs - group * a.ks;
   const int n0 = group * CW;
-  if (slab > 0) {
+  if (SLABS && slab > 0) {
     const int64_t r0 = 32 * (int64_t)slab;
     a.x += a.x_tiled ? 2 * slab * (int64_t)(a.k >> 5) * 512 : r0 * a.x_stride;
     if (NORM) a.x_ssq += r0 * (a.k >> 5);
@@ -132,7 +132,7 @@ skinny_gemm_kernel(GemmArgs a) {
     a.partials += (int64_t)slab * groups * a.ks * NACC * TF;
     a.m -= 32 * slab;
   }
-  a.m = min(a.m, 32);
+  if (SLABS) a.m = min(a.m, 32);
 
   // Operand addresses: base + k0 * step for the 32-wide K step starting at k0 (tiled: the
   // step's 512-element tile follows the previous one, so 16 elements per unit of k).
@@ -144,7 +144,7 @@ skinny_gemm_kernel(GemmArgs a) {
     xr[mt] = min(16 * mt + n, a.m - 1);
     // a tiled X holds 16 * ceil(M/16) rows: an M tile past the slab's last row re-reads its last
     // tile (those rows only reach dropped outputs)
-    const int mt_x = min(mt, (a.m - 1) >> 4);
+    const int mt_x = SLABS ? min(mt, (a.m - 1) >> 4) : mt;
     xp[mt] = a.x_tiled ? a.x + (int64_t)mt_x * (a.k >> 5) * 512 + 8 * lane : a.x + (int64_t)xr[mt] * a.x_stride + 8 * g;
   }
   const u16 *wp[NACC];
@@ -354,10 +354,15 @@ size_t workspace_bytes_for(const Plan &p, int n, int epi) {
 
 template <int NW, int KB, int NT, int EPI, bool NORM>
 int launch(const GemmArgs &a, int grid, hipStream_t stream) {
-  if (a.m > 16)
-    hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 2, EPI, NORM>), dim3(grid), dim3(NW * 64), 0, stream, a);
+  if (a.m > 32)
+    hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 2, EPI, NORM, true>), dim3(grid), dim3(NW * 64), 0, stream,
+                       a);
+  else if (a.m > 16)
+    hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 2, EPI, NORM, false>), dim3(grid), dim3(NW * 64), 0, stream,
+                       a);
   else
-    hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 1, EPI, NORM>), dim3(grid), dim3(NW * 64), 0, stream, a);
+    hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 1, EPI, NORM, false>), dim3(grid), dim3(NW * 64), 0, stream,
+                       a);
   return launch_status();
 }
 
