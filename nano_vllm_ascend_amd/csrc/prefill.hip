@@ -95,6 +95,15 @@ __device__ __forceinline__ u32 lds_addr(const u16 *p) {
   return (u32)(uintptr_t)(const __attribute__((address_space(3))) u16 *)p;
 }
 
+// max over lanes l and l ^ 32 of a score maximum (finite or -inf, never NaN: v_max_f32 without
+// the canonicalising moves fmaxf adds to the permuted operands)
+__device__ __forceinline__ float max_swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(r[0])), "v"(__uint_as_float(r[1])));
+  return m;
+}
+
 __device__ __forceinline__ f32x16 mfma32(bf16x8v a, bf16x8v b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -149,7 +158,11 @@ prefill_kernel(PrefillArgs a) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // Exponent reference per query column (log2 units of scaled scores), the threshold above
+  // which it moves, and -reference.  The finite start needs no guard in the exponent: while a
+  // lane has seen only masked (-inf) scores its arguments stay -inf, and its first finite score
+  // moves the reference.  The first visible tile of a wave is tile 0.
+  float m_ref = -1e30f, m_thr = -1e30f, neg_ref = 1e30f, l_run = 0.f;
 
   // Keys this workgroup needs: up to the last visible key of its last valid row.
   const int kv_hi = min(kv_len, offset + min((qt + 1) * BQ, q_len));
@@ -299,17 +312,28 @@ prefill_kernel(PrefillArgs a) {
       float tmax = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sc[i]);
-      tmax = max_xor32(tmax) * a.scale_log2e;
+      tmax = max_swap32(tmax) * a.scale_log2e;
       // Lazy rescale: the exponent's reference moves only when a score exceeds it by more
       // than 2^8, so P <= 256 and O, l are rescaled only on the tiles where some lane's
-      // reference moved.  O / l is unchanged by the choice of reference.
-      float alpha = 1.f;
-      if (tmax > m_run + kRescaleLog2) {
-        alpha = __builtin_amdgcn_exp2f(m_run - tmax);  // 0 on the first visible tile
-        m_run = tmax;
+      // reference moved (a wave-uniform branch, taken on the first tile and rarely after).
+      // O / l is unchanged by the choice of reference.  On the first tile O and l are still
+      // zero and need no scaling.
+      if (__builtin_amdgcn_ballot_w64(tmax > m_thr) != 0) {
+        const bool up = tmax > m_thr;
+        const float alpha = up ? __builtin_amdgcn_exp2f(m_ref - tmax) : 1.f;
+        if (up) {
+          m_ref = tmax;
+          m_thr = tmax + kRescaleLog2;
+          neg_ref = -tmax;
+        }
+        if (t > 0) {
+          l_run *= alpha;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+        }
       }
-      const float neg_ref = m_run == -INFINITY ? 0.f : -m_run;
-      float psum = 0.f;
       bf16x8v pf[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -318,19 +342,11 @@ prefill_kernel(PrefillArgs a) {
         for (int e = 0; e < 4; ++e) {
           const u32 pr = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[8 * hh + 2 * e], a.scale_log2e, neg_ref)),
                                      __builtin_amdgcn_exp2f(fmaf(sc[8 * hh + 2 * e + 1], a.scale_log2e, neg_ref)));
-          psum = dot2_bf16(pr, kBf16PairOne, psum);  // both rounded values of the pair
+          l_run = dot2_bf16(pr, kBf16PairOne, l_run);  // both rounded values of the pair
           packed[e] = pr;
         }
         pf[hh] = __builtin_bit_cast(bf16x8v, packed);
       }
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {  // wave-uniform
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-      }
-      l_run += psum;
 
       // O^T += V^T P^T, two 16-key steps
 #pragma unroll
@@ -352,7 +368,7 @@ prefill_kernel(PrefillArgs a) {
   // normalise and write: register i of block db is dim 32db + 8(i/4) + 4hl + i%4 of query column n
   const float l_tot = sum_xor32(l_run);
   if (!q_ok) return;
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float inv = l_tot > 0.f ? __builtin_amdgcn_rcpf(l_tot) : 0.f;  // v_rcp_f32 (1 ulp): output is bf16
   u16 *op = a.out + q_tok * a.out_stride + (int64_t)head * D + 4 * hl;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
