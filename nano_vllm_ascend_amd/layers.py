@@ -209,7 +209,7 @@ def _skinny_ok(x: torch.Tensor, weight: torch.Tensor, tiled: torch.Tensor | None
 
 def linear(x: torch.Tensor, weight: torch.Tensor, skinny: bool = True,
            tiled: torch.Tensor | None = None) -> torch.Tensor:
-    """x @ weight^T.  Batches of <= 32 rows use the skinny-M HIP kernel when the weight's tiled
+    """x @ weight^T.  Batches of <= 128 rows use the skinny-M HIP kernel when the weight's tiled
     copy (``_C.tile(weight)``) is given -- it streams the weight once; otherwise, and for larger
     batches (prefill), the library GEMM.  ``skinny=False`` keeps a projection on the library GEMM."""
     if skinny and _skinny_ok(x, weight, tiled):
@@ -219,7 +219,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, skinny: bool = True,
 
 def gate_up_silu(x: torch.Tensor, w_gate_up: torch.Tensor, tiled: torch.Tensor | None = None) -> torch.Tensor:
     """silu(x @ W_gate^T) * (x @ W_up^T) for the fused [2I, H] weight (nv/models/qwen3.py:34-35):
-    one HIP launch for batches of <= 32 rows when the weight's tiled copy is given, library GEMM +
+    one HIP launch for batches of <= 128 rows when the weight's tiled copy is given, library GEMM +
     silu_mul kernel otherwise."""
     if _skinny_ok(x, w_gate_up, tiled) and (w_gate_up.shape[0] // 2) % 32 == 0:
         return _C.linear_silu_mul(x, tiled)
