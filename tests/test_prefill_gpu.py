@@ -51,6 +51,35 @@ def test_dense_prefill_gqa_groups(device, heads):
     assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
+def _ramped(lens, device, seed, key_gain, q_gain=1.0):
+    """q/k/v for `lens` with every sequence's keys scaled by key_gain(position): the running score
+    maximum then rises tile after tile, past the kernel's lazy-rescale threshold (2^8) several times."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    t = sum(lens)
+    q = (torch.randn((t, 16, 128), generator=gen, device=device) * q_gain).to(torch.bfloat16)
+    k = torch.randn((t, 8, 128), generator=gen, device=device)
+    pos = torch.cat([torch.arange(n, device=device) for n in lens]).float()
+    k = (k * key_gain(pos)[:, None, None]).to(torch.bfloat16)
+    v = rand((t, 8, 128), gen, device)
+    return q, k, v
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["ramp", "large"])
+def test_dense_prefill_rescales_after_the_first_tile(device, case):
+    """Scores that grow along the keys (ramp) or are large everywhere (q and k ~ N(0, 9)): the
+    exponent reference moves on later tiles, so O and l are rescaled mid-sequence."""
+    lens = [300, 1000, 64]
+    gain = (lambda pos: 1.0 + pos / 48.0) if case == "ramp" else (lambda pos: torch.full_like(pos, 3.0))
+    q, k, v = _ramped(lens, device, seed=21, key_gain=gain, q_gain=1.0 if case == "ramp" else 3.0)
+    cu = W.cu_seqlens(lens)
+    out = torch.empty_like(q)
+    _C.varlen_prefill(out, q, k, v, torch.tensor(cu, dtype=torch.int32, device=device), max(lens), SCALE)
+    torch.cuda.synchronize()
+    ref = varlen_prefill_ref(q, k, v, cu, SCALE)
+    assert (out.float().cpu() - ref).abs().max().item() <= TOL
+
+
 @pytest.mark.gpu
 def test_dense_prefill_fused_qkv_views(device):
     out, q, k, v, cu = run_dense([70, 150], 16, 8, device, seed=9, fused=True)
@@ -115,6 +144,41 @@ def test_paged_prefix_hit_prefill(device, bs):
                       SCALE)
     torch.cuda.synchronize()
     assert (out.float() - dense[sel].float()).abs().max().item() <= TOL
+
+
+@pytest.mark.gpu
+def test_paged_prefill_rescales_after_the_first_tile(device):
+    """The paged route's softmax with keys that grow along the prompt (reference moves on later tiles)."""
+    prompt_lens = [700, 300]
+    cached = [512, 128]
+    bs = 64
+    q, k, v = _ramped(prompt_lens, device, seed=5, key_gain=lambda pos: 1.0 + pos / 48.0)
+    num_blocks = 64
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(5)).tolist()
+    width = max(math.ceil(n / bs) for n in prompt_lens)
+    tables = torch.zeros((len(prompt_lens), width), dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(prompt_lens):
+        nb = math.ceil(n / bs)
+        tables[i, :nb] = torch.tensor(perm[at : at + nb])
+        at += nb
+    kc = torch.full((num_blocks, bs, 8, 128), float("nan"), dtype=torch.bfloat16, device=device)
+    vc = torch.full_like(kc, float("nan"))
+    slots = torch.tensor([int(tables[i, p // bs]) * bs + p % bs for i, n in enumerate(prompt_lens) for p in range(n)],
+                         dtype=torch.int64, device=device)
+    _C.kv_cache_write(k, v, kc, vc, slots)
+    cu_full = W.cu_seqlens(prompt_lens)
+    sel = torch.tensor([cu_full[i] + p for i, n in enumerate(prompt_lens) for p in range(cached[i], n)],
+                       device=device)
+    qs = q[sel].contiguous()
+    q_lens = [n - c for n, c in zip(prompt_lens, cached)]
+    cu_q = W.cu_seqlens(q_lens)
+    out = torch.empty_like(qs)
+    _C.paged_prefill(out, qs, kc, vc, tables.to(device), torch.tensor(cu_q, dtype=torch.int32, device=device),
+                     torch.tensor(prompt_lens, dtype=torch.int32, device=device), max(q_lens), SCALE)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(qs, kc, vc, tables, cu_q, prompt_lens, SCALE)
+    assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
 @pytest.mark.gpu
