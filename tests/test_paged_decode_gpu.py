@@ -65,6 +65,27 @@ def test_decode_long_contexts_many_partitions(device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("case", ["ramp", "large"])
+def test_decode_partitions_with_far_apart_maxima(device, case):
+    """Keys scaled up along each context (ramp: later partitions' maxima exceed earlier ones by tens
+    of log2 units, so the merge weighs early partitions by ~0 and the running maximum moves inside
+    partitions) or large everywhere (q and k ~ N(0, 9))."""
+    work = W.make_decode(8, 1000, 3000, 200, seed=31, device=device)
+    bs = work.key_cache.shape[2]
+    if case == "ramp":
+        for i, n in enumerate(work.context_lens_list):
+            pos = torch.arange(n, device=device)
+            blocks = work.block_tables[i, pos // bs].long()
+            gain = (1.0 + pos.float() / 64.0)[:, None, None]
+            rows = work.key_cache[0, blocks, pos % bs].float()
+            work.key_cache[0, blocks, pos % bs] = (rows * gain).to(torch.bfloat16)
+    else:
+        work.key_cache[0].mul_(3.0)
+        work.q.mul_(3.0)
+    check(work)
+
+
+@pytest.mark.gpu
 def test_decode_large_ragged_batch_with_empty_sequences(device):
     """150 sequences (the work list spans three 64-sequence scans), some with no context."""
     gen = torch.Generator().manual_seed(21)
