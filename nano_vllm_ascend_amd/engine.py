@@ -56,13 +56,17 @@ class LLM:
     ``num_blocks`` the KV pool takes ``npu_memory_utilization`` of device
     memory.  ``enable_overlap`` (not in the reference) lets the runner launch
     a decode step before the host has read the previous step's tokens; tokens
-    and packing metadata are those of the synchronous loop.
+    and packing metadata are those of the synchronous loop.  ``retain_logits``
+    (not in the reference, which exposes no logits) keeps every step's logits
+    readable as ``runner.last_logits``, at one logits-sized copy per overlapped
+    step.
     """
 
     def __init__(self, model_path, max_model_len: int = 2048, block_size: int = 128, num_blocks: int | None = None,
                  max_num_seqs: int = 4, device_id: int = 0, npu_memory_utilization: float = 0.8,
                  enable_prefix_cache: bool = False, enable_decode_graph: bool = True,
-                 decode_graph_batch_sizes: list[int] | None = None, seed: int = 0, enable_overlap: bool = True):
+                 decode_graph_batch_sizes: list[int] | None = None, seed: int = 0, enable_overlap: bool = True,
+                 retain_logits: bool = False):
         from .model_runner import ModelRunner
 
         self.runner = ModelRunner(
@@ -70,7 +74,7 @@ class LLM:
             device_id=device_id, npu_memory_utilization=npu_memory_utilization,
             enable_prefix_cache=enable_prefix_cache, enable_decode_graph=enable_decode_graph,
             decode_graph_batch_sizes=decode_graph_batch_sizes, seed=seed, max_num_seqs=max_num_seqs,
-            enable_overlap=enable_overlap)
+            enable_overlap=enable_overlap, retain_logits=retain_logits)
         self.scheduler = MiniScheduler(max_num_seqs=max_num_seqs, block_size=block_size,
                                        total_num_blocks=self.runner.num_blocks)
         self.engine_core = EngineCore(self.runner, self.scheduler)

@@ -102,8 +102,11 @@ class DecodeGraphRunner:
             "slot_mapping": torch.zeros(b, dtype=torch.int64, device=device),
             "cu_seqlens_q": torch.zeros(b + 1, dtype=torch.int32, device=device),
             "last_token_indices": torch.zeros(b, dtype=torch.int64, device=device),
-            "greedy_ids": torch.zeros(b, dtype=torch.int64, device=device),  # in-graph argmax of the logits
         }
+        # In-graph argmax of the logits, written over the input ids: the embedding has read them by
+        # then, so a replay launched right behind this one takes this step's tokens as its inputs
+        # without a copy (a host-packed step writes its own ids before its replay).
+        bufs["greedy_ids"] = bufs["input_ids"]
         cfg = getattr(self.model, "config", None)
         hq = getattr(cfg, "num_attention_heads", 1)
         hkv = getattr(cfg, "num_key_value_heads", 1)

@@ -11,9 +11,11 @@ Differences from the reference, all on the hot path:
   - overlapped decode: when step N+1's batch is predictable before step N's
     tokens reach the host (every sequence continues unless it samples EOS,
     nothing was prefilled in between, greedy sampling, a captured batch
-    size), step N+1 is launched right behind step N with its input ids copied
-    on the device from step N's argmax, and the host reads step N's tokens and
-    plans the next engine step while the GPU runs.  Step N+1 is packed ahead
+    size), step N+1 is launched right behind step N with step N's argmax as
+    its input ids (the graph writes the argmax over its input-id buffer), and
+    the host reads step N's tokens and plans the next engine step while the
+    GPU runs.  ``last_logits`` of such a step is None unless ``retain_logits``
+    asks for a copy (the static logits buffer belongs to the step launched).  Step N+1 is packed ahead
     WITHOUT touching the block pool: a sequence that crosses into a new block
     uses the block the pool would hand out next (the front of the free queue
     in batch order), which is the block the synchronous loop allocates if
@@ -105,7 +107,7 @@ class ModelRunner:
     def __init__(self, model_path, max_model_len: int, num_blocks: int | None, block_size: int, device_id: int,
                  npu_memory_utilization: float, enable_prefix_cache: bool = False, enable_decode_graph: bool = False,
                  decode_graph_batch_sizes: list[int] | None = None, seed: int = 0, max_num_seqs: int = 64,
-                 enable_overlap: bool = True):
+                 enable_overlap: bool = True, retain_logits: bool = False):
         torch.cuda.set_device(device_id)
         self.device = torch.device("cuda", device_id)
         self.model_path = model_path
@@ -115,7 +117,7 @@ class ModelRunner:
         self.sampler = Sampler()
         self.enable_prefix_cache = enable_prefix_cache
         self.enable_decode_graph = enable_decode_graph
-        self._init_step_state(enable_overlap)
+        self._init_step_state(enable_overlap, retain_logits)
         self.config = load_config(model_path)
         self.tokenizer = _load_tokenizer(model_path, self.config.eos_token_id)
 
@@ -134,9 +136,10 @@ class ModelRunner:
                 batch_sizes=decode_graph_batch_sizes or DEFAULT_DECODE_GRAPH_BATCH_SIZES,
                 max_model_len=max_model_len, block_size=block_size)
 
-    def _init_step_state(self, enable_overlap: bool) -> None:
+    def _init_step_state(self, enable_overlap: bool, retain_logits: bool = False) -> None:
         """Per-step bookkeeping: last logits, the step launched ahead, token fetch buffers."""
         self.last_logits: torch.Tensor | None = None
+        self.retain_logits = retain_logits  # keep overlapped steps' logits readable (a copy per step)
         self.enable_overlap = enable_overlap
         self._in_flight: _InFlightStep | None = None
         self._prefilled_since_decode = False
@@ -342,27 +345,28 @@ class ModelRunner:
         self._prefilled_since_decode, prefilled = False, self._prefilled_since_decode
         admits = self.next_step_admits is not None and self.next_step_admits()
         if entry is not None and fetch is not None and not prefilled and not admits and self._can_launch_ahead(seqs):
-            logits = self._launch_ahead(seqs, positions, tokens, entry, logits)
+            logits = self._launch_ahead(seqs, positions, entry, logits)
         self.last_logits = logits
         ids = fetch.tokens() if fetch is not None else self._sample(logits, seqs)
         for seq, token in zip(seqs, ids):
             seq.set_decode_result(token)
 
-    def _launch_ahead(self, seqs, positions, tokens, entry, logits) -> torch.Tensor:
+    def _launch_ahead(self, seqs, positions, entry, logits) -> torch.Tensor | None:
         """Launch step N+1 behind step N: same sequences, next positions, input ids = step N's
-        argmax (device to device).  Returns step N's logits, copied out of the static buffer
-        the launched replay overwrites (unchanged when nothing is launched)."""
+        argmax (the graph writes it over its input ids).  Returns step N's logits: unchanged when
+        nothing is launched, else copied out of the static buffer the launched replay overwrites
+        when ``retain_logits`` is set, and None otherwise (only greedy steps launch ahead, so
+        nothing else reads them)."""
         b = len(seqs)
         nxt = [p + 1 for p in positions]
-        packed = self.block_manager.prepare_decode_ahead([seq.seq_id for seq in seqs], nxt, token_ids=tokens,
+        packed = self.block_manager.prepare_decode_ahead([seq.seq_id for seq in seqs], nxt, token_ids=None,
                                                          width=entry.width, out=entry.buffers)
         if packed is None:
             return logits
         md, taken = packed
-        kept = self._keep_logits(b, logits)
+        kept = self._keep_logits(b, logits) if self.retain_logits else None
         snapshot = self._host_metadata(md) if self.metadata_hook is not None else None
-        entry.buffers["input_ids"].copy_(entry.buffers["greedy_ids"])
-        nxt_logits = self.decode_graph_runner.replay(entry)
+        nxt_logits = self.decode_graph_runner.replay(entry)  # its input ids: step N's argmax, in place
         self._in_flight = _InFlightStep(seqs, nxt, taken, entry, self._fetch_tokens(b, entry.buffers["greedy_ids"]),
                                         nxt_logits, snapshot)
         self.overlap_stats["launched"] += 1

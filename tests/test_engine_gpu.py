@@ -21,7 +21,7 @@ def prompts_for(lens, seed=0):
 
 def make_llm(graph=True, prefix=False, layers=SMALL, num_blocks=96, max_num_seqs=8, seed=1, max_model_len=1024):
     return LLM(layers, max_model_len=max_model_len, num_blocks=num_blocks, max_num_seqs=max_num_seqs,
-               enable_decode_graph=graph, enable_prefix_cache=prefix, seed=seed)
+               enable_decode_graph=graph, enable_prefix_cache=prefix, seed=seed, retain_logits=True)
 
 
 # Random N(0, 0.02) weights give logits with std ~0.64 over 151,936 tokens, so the
@@ -143,7 +143,7 @@ def test_full_depth_greedy_tokens_against_oracle(device):
 
     steps = 33
     prompts = make_dataset(32, 256, QWEN3_0_6B.vocab_size, seed=0)
-    llm = LLM(QWEN3_0_6B, max_model_len=2304, num_blocks=32 * 3 + 8, max_num_seqs=32, seed=0)
+    llm = LLM(QWEN3_0_6B, max_model_len=2304, num_blocks=32 * 3 + 8, max_num_seqs=32, seed=0, retain_logits=True)
     llm.runner.tokenizer.eos_token_id = -1
     ids = [llm.submit(p, max_new_tokens=steps) for p in prompts]
     step_logits = []

@@ -26,7 +26,8 @@ TIE_TOL = 0.05
 
 def make(prefix: bool) -> LLM:
     llm = LLM(SMALL, max_model_len=4096, block_size=128, num_blocks=N * 17 + 32, max_num_seqs=N,
-              enable_prefix_cache=prefix, decode_graph_batch_sizes=[1, 2, 4, 8, 16, 32, 64, 100], seed=1)
+              enable_prefix_cache=prefix, decode_graph_batch_sizes=[1, 2, 4, 8, 16, 32, 64, 100], seed=1,
+              retain_logits=True)
     llm.runner.tokenizer.eos_token_id = -1
     return llm
 
