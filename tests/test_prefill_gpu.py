@@ -97,8 +97,9 @@ def test_dense_prefill_32_ragged_prompts(device):
     assert err <= TOL, err
 
 
-def _paged_case(device, prompt_lens, cached, bs=128, seed=0, hq=16, hkv=8):
-    """Full prompts written to a paged cache; queries = the suffix after `cached` tokens."""
+def _paged_case(device, prompt_lens, cached, bs=128, seed=0, hq=16, hkv=8, qkv=None):
+    """Full prompts written to a paged cache; queries = the suffix after `cached` tokens.  `qkv`
+    gives the prompts' (q, k, v) instead of seeded N(0, 1) ones."""
     gen = torch.Generator(device=device).manual_seed(seed)
     nblk = [math.ceil(n / bs) for n in prompt_lens]
     num_blocks = sum(nblk) + 3
@@ -109,9 +110,12 @@ def _paged_case(device, prompt_lens, cached, bs=128, seed=0, hq=16, hkv=8):
         tables[i, :nb] = torch.tensor(perm[pos : pos + nb])
         pos += nb
     t = sum(prompt_lens)
-    q = rand((t, hq, 128), gen, device)
-    k = rand((t, hkv, 128), gen, device)
-    v = rand((t, hkv, 128), gen, device)
+    if qkv is None:
+        q = rand((t, hq, 128), gen, device)
+        k = rand((t, hkv, 128), gen, device)
+        v = rand((t, hkv, 128), gen, device)
+    else:
+        q, k, v = qkv
     kc = torch.full((num_blocks, bs, hkv, 128), float("nan"), dtype=torch.bfloat16, device=device)
     vc = torch.full_like(kc, float("nan"))
     slots = torch.tensor([int(tables[i, p // bs]) * bs + p % bs for i, n in enumerate(prompt_lens) for p in range(n)],
@@ -149,34 +153,10 @@ def test_paged_prefix_hit_prefill(device, bs):
 @pytest.mark.gpu
 def test_paged_prefill_rescales_after_the_first_tile(device):
     """The paged route's softmax with keys that grow along the prompt (reference moves on later tiles)."""
-    prompt_lens = [700, 300]
-    cached = [512, 128]
-    bs = 64
-    q, k, v = _ramped(prompt_lens, device, seed=5, key_gain=lambda pos: 1.0 + pos / 48.0)
-    num_blocks = 64
-    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(5)).tolist()
-    width = max(math.ceil(n / bs) for n in prompt_lens)
-    tables = torch.zeros((len(prompt_lens), width), dtype=torch.int32)
-    at = 0
-    for i, n in enumerate(prompt_lens):
-        nb = math.ceil(n / bs)
-        tables[i, :nb] = torch.tensor(perm[at : at + nb])
-        at += nb
-    kc = torch.full((num_blocks, bs, 8, 128), float("nan"), dtype=torch.bfloat16, device=device)
-    vc = torch.full_like(kc, float("nan"))
-    slots = torch.tensor([int(tables[i, p // bs]) * bs + p % bs for i, n in enumerate(prompt_lens) for p in range(n)],
-                         dtype=torch.int64, device=device)
-    _C.kv_cache_write(k, v, kc, vc, slots)
-    cu_full = W.cu_seqlens(prompt_lens)
-    sel = torch.tensor([cu_full[i] + p for i, n in enumerate(prompt_lens) for p in range(cached[i], n)],
-                       device=device)
-    qs = q[sel].contiguous()
-    q_lens = [n - c for n, c in zip(prompt_lens, cached)]
-    cu_q = W.cu_seqlens(q_lens)
-    out = torch.empty_like(qs)
-    _C.paged_prefill(out, qs, kc, vc, tables.to(device), torch.tensor(cu_q, dtype=torch.int32, device=device),
-                     torch.tensor(prompt_lens, dtype=torch.int32, device=device), max(q_lens), SCALE)
-    torch.cuda.synchronize()
+    prompt_lens, cached = [700, 300], [512, 128]
+    qkv = _ramped(prompt_lens, device, seed=5, key_gain=lambda pos: 1.0 + pos / 48.0)
+    out, qs, q, k, v, kc, vc, tables, cu_q, cu_full, sel = _paged_case(device, prompt_lens, cached, bs=64, seed=5,
+                                                                       qkv=qkv)
     ref = paged_prefill_ref(qs, kc, vc, tables, cu_q, prompt_lens, SCALE)
     assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
