@@ -249,15 +249,17 @@ def run_scenario(name, *, BlockManager, MiniScheduler, EngineCore, Sequence, Sam
 
 
 def run_schedule(schedule, token_fn, eos_token_id, *, block_size, num_blocks, max_num_seqs, prefix_cache,
-                 BlockManager, MiniScheduler, EngineCore, Sequence, SamplingParams, torch_mod, device="cpu"):
+                 BlockManager, MiniScheduler, EngineCore, Sequence, SamplingParams, torch_mod, device="cpu",
+                 events=None):
     """Drive an engine from a submission schedule and a token stream; return the recorded events.
 
     ``schedule`` maps an engine step index to the (prompt token ids, max_new_tokens) submitted
     just before that step runs; ``token_fn(seq_id, n)`` is the token request ``seq_id`` samples
     as its token number n (EOS included).  Steps run until nothing is left and no submission
-    is pending.
+    is pending.  Events go to ``events`` when given, so a caller keeps those recorded before
+    an exception.
     """
-    events = []
+    events = [] if events is None else events
     bm = BlockManager(num_blocks=num_blocks, block_size=block_size, device=device)
     runner = TraceRunner(bm, block_size, prefix_cache, torch_mod, events.append, token_fn=token_fn)
     sched = MiniScheduler(max_num_seqs=max_num_seqs, block_size=block_size, total_num_blocks=num_blocks)

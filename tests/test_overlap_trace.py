@@ -18,6 +18,7 @@
 from __future__ import annotations
 
 import json
+import random
 import sys
 from pathlib import Path
 from types import SimpleNamespace
@@ -261,6 +262,61 @@ def test_overlapped_runner_metadata_equals_oracle_replay(monkeypatch, case):
     assert stats["launched"] > 0 and stats["used"] > 0, stats
     if case == "bs128":  # EOS found while the next step was in flight: launches were discarded
         assert stats["discarded"] > 0, stats
+    ref = oracle_replay(schedule, out, reasons, eos, **cfg)
+    assert_same_metadata(sync_events, ref)
+    assert_same_metadata(events, ref)
+
+
+def _dry_pool_run(schedule, cfg, monkeypatch):
+    """Run a schedule on which the reference's reservation over-commits the pool: the oracle and
+    both product loops must raise the same error after the same packing metadata.
+
+    The reference reserves blocks for the uncached prompt suffix plus the output budget only
+    (src/nanovllm_ascend/engine.py:161-164), while a prefix hit takes its cached blocks off the
+    free queue, so a tight pool can run dry in a later decode."""
+    ref_events = []
+    with pytest.raises(RuntimeError, match="out of free blocks"):
+        trace_driver.run_schedule(schedule, lambda seq_id, n: 1, -1, block_size=cfg["block_size"],
+                                  num_blocks=cfg["num_blocks"], max_num_seqs=cfg["max_num_seqs"],
+                                  prefix_cache=cfg["prefix"], events=ref_events, **ORACLE)
+    ref = [e for e in ref_events if e["event"] in ("prefill", "decode")]
+    for overlap in (False, True):
+        events = []
+        with pytest.raises(RuntimeError, match="out of free blocks"):
+            run_product(make_llm(monkeypatch, overlap=overlap, **cfg), schedule, -1, events=events)
+        assert_same_metadata(events, ref)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_overlapped_runner_random_schedules_equal_oracle_replay(monkeypatch, seed):
+    """Seeded random configurations (block size, a tight pool, slots, prefix cache, arrivals,
+    lengths, shared prefixes, an EOS token): the overlapped runner's tokens and every step's
+    packing metadata equal the synchronous loop's and the oracle's replay of the same run.
+    Where the reference's own accounting runs the pool dry (seed 10), all three raise alike."""
+    rng = random.Random(1000 + seed)
+    bs = rng.choice([16, 32, 128])
+    n = rng.randint(5, 12)
+    len_hi = rng.randint(bs // 2, 3 * bs)
+    new_hi = rng.randint(4, 2 * bs)
+    shared = rng.choice([0, 1, 2])
+    per_req = -(-(shared * bs + len_hi + new_hi) // bs)  # blocks of the largest request
+    cfg = dict(block_size=bs, num_blocks=per_req + rng.randint(0, 3 * per_req), max_num_seqs=rng.randint(2, 6),
+               prefix=rng.random() < 0.5)
+    schedule = make_schedule(seed, n, bs, 1, len_hi, 1, new_hi, shared)
+    try:  # without EOS, scheduling does not depend on the tokens
+        trace_driver.run_schedule(schedule, lambda seq_id, n: 1, -1, block_size=bs, num_blocks=cfg["num_blocks"],
+                                  max_num_seqs=cfg["max_num_seqs"], prefix_cache=cfg["prefix"], **ORACLE)
+    except RuntimeError as e:
+        assert "out of free blocks" in str(e)
+        _dry_pool_run(schedule, cfg, monkeypatch)
+        return
+    _, plain, _ = run_product(make_llm(monkeypatch, overlap=False, **cfg), schedule, -1)
+    longest = max(plain.values(), key=len)
+    eos = longest[len(longest) // 2] if len(longest) > 2 else -1
+    sync_events, sync_out, sync_reasons = run_product(make_llm(monkeypatch, overlap=False, **cfg), schedule, eos)
+    llm = make_llm(monkeypatch, overlap=True, **cfg)
+    events, out, reasons = run_product(llm, schedule, eos)
+    assert out == sync_out and reasons == sync_reasons
     ref = oracle_replay(schedule, out, reasons, eos, **cfg)
     assert_same_metadata(sync_events, ref)
     assert_same_metadata(events, ref)

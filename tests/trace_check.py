@@ -39,9 +39,9 @@ def make_schedule(seed, n, block_size, len_lo, len_hi, new_lo, new_hi, shared_bl
     return schedule
 
 
-def run_product(llm, schedule, eos):
+def run_product(llm, schedule, eos, events=None):
     llm.runner.tokenizer.eos_token_id = eos
-    events = []
+    events = [] if events is None else events
 
     def hook(kind, slots, md):
         events.append({"event": kind, "slots": slots, "block_tables": md.block_tables.tolist(),
