@@ -12,7 +12,8 @@ them.  Inputs are resident in HBM before the timed region.
 Also reported: the roofline of the decode kernel (average launch duration from
 HIP events on the launch stream), the fp32 CPU oracle on the host cores as the
 CPU baseline, the same decode step with the per-head q/k norm, RoPE and KV store fused into
-the attention launch (against the two-launch chain), the ragged causal prefill of 32 prompts of U[64, 2048] tokens
+the attention launch (against the two-launch chain), the same kernel at larger decode shapes (up
+to the load workload's 100 sequences x U[2048, 4096]), the ragged causal prefill of 32 prompts of U[64, 2048] tokens
 (TFLOP/s against the dense bf16 MFMA peak) with its paged KV store (GB/s), and
 (unless --no-e2e) the end-to-end output tok/s of the 32 x 256-in / 2048-out
 greedy workload and of the 100 x 2048 / 2048 load workload (half the requests share
@@ -285,6 +286,58 @@ def small_decode_leg(args, device) -> dict:
                           "note": "latency-bound: one small launch"},
         "work": work,
     }
+
+
+# Larger decode shapes for the same kernel: batch and context ranges of the 32-sequence step at twice
+# the batch, at the load workload's context range (2048 prompt tokens + up to 2048 generated), and at
+# that workload's batch of 100.  Each shape rotates over `layers` pools whose summed read set is far
+# beyond the 256 MB Infinity Cache.
+SCALING_SHAPES = ((64, 256, 2304, 14), (32, 2048, 4096, 10), (100, 2048, 4096, 4))
+
+
+def decode_scaling_leg(args, device) -> list[dict]:
+    """GB/s of the decode kernel at the larger shapes (average over launches, HIP events on the
+    launch stream, as for `value`): how much of the 32-sequence step's gap to the HBM peak is the
+    launch's fixed ramp and merge tail, which larger launches amortise."""
+    import torch
+
+    from nano_vllm_ascend_amd import _C
+    from nano_vllm_ascend_amd import workloads as W
+
+    rows = []
+    for batch, lo, hi, layers in SCALING_SHAPES:
+        work = W.make_decode(batch, lo, hi, batch * -(-hi // W.BLOCK_SIZE) + 8, args.seed, device, num_layers=layers)
+        max_ctx = max(work.context_lens_list)
+        ws = _C.alloc_paged_decode_workspace(batch, W.NUM_HEADS, W.NUM_KV_HEADS, max_ctx, device)
+        out = torch.empty_like(work.q)
+        nbytes = (sum(work.context_lens_list) * W.NUM_KV_HEADS * W.HEAD_DIM * 2 * 2
+                  + 2 * batch * W.NUM_HEADS * W.HEAD_DIM * 2 + batch * work.block_tables.shape[1] * 4 + batch * 4)
+        scale = W.HEAD_DIM ** -0.5
+
+        def step():
+            for layer in range(layers):
+                _C.paged_decode(out, work.q, work.key_cache[layer], work.value_cache[layer], work.block_tables,
+                                work.context_lens, scale, max_ctx, ws)
+
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        reps = max(5, args.steps * NUM_LAYERS // layers)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / (reps * layers)
+        gbs = nbytes / us / 1e3
+        rows.append({"workload": f"decode {batch} seqs, context U[{lo}, {hi}] (sum {sum(work.context_lens_list)}), "
+                                 f"{layers} layer pools",
+                     "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3), "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del work, ws, out
+        torch.cuda.empty_cache()
+    return rows
 
 
 def prefill_leg(args, device) -> dict:
@@ -671,6 +724,7 @@ def main():
     result["pack"] = pack_leg(args, device)
     small = small_decode_leg(args, device)
     result["decode_small"] = {k: v for k, v in small.items() if k != "work"}
+    result["decode_scaling"] = decode_scaling_leg(args, device)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(dec["work"], args.seed)
         result["cpu_baseline_other"] = cpu_baselines_other(small["work"], args.seed)
