@@ -172,6 +172,20 @@ skinny_gemm_kernel(GemmArgs a) {
     }
   }
 
+  // RESID: the residual values this thread adds in the epilogue (work unit u = tid, see there),
+  // read now so that their load overlaps the weight stream instead of following the merge.  Only
+  // this column group's merging workgroup writes them, after every read of this launch.
+  constexpr int kRowUnits = CW / 4;
+  static_assert(EPI != kEpiResid || 32 * kRowUnits <= kNW * 64, "RESID: one epilogue unit per thread");
+  u32x2 resid = {0u, 0u};
+  if constexpr (EPI == kEpiResid) {
+    if (tid < 32 * kRowUnits) {
+      const int rr = min(tid / kRowUnits, a.m - 1);
+      const int c = n0 + 4 * (tid % kRowUnits);
+      resid = *reinterpret_cast<const u32x2 *>(a.y + (a.y_tiled ? tiled_index(rr, c, a.n) : (int64_t)rr * a.y_stride + c));
+    }
+  }
+
   f32x4 acc[NACC][MT];
 #pragma unroll
   for (int t = 0; t < NACC; ++t)
@@ -256,7 +270,6 @@ skinny_gemm_kernel(GemmArgs a) {
 
   // Work unit u: 4 consecutive columns of one output row; the 8 units of 32 columns of a
   // row sit in 8 consecutive lanes.
-  constexpr int kRowUnits = CW / 4;
   for (int u = tid; u < 32 * kRowUnits; u += kNW * 64) {
     const int row = u / kRowUnits;
     const int cl = 4 * (u % kRowUnits);  // column inside the workgroup's CW
@@ -295,9 +308,7 @@ skinny_gemm_kernel(GemmArgs a) {
       for (int q = 0; q < 4; ++q) o[q] = round_bf16(silu_f32(round_bf16(v[0][q]))) * round_bf16(v[NV - 1][q]);
       if (row < a.m) *reinterpret_cast<u32x2 *>(yp) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     } else {  // RESID
-      const int rr = min(row, a.m - 1);
-      const u32x2 r = *reinterpret_cast<const u32x2 *>(
-          a.y + (a.y_tiled ? tiled_index(rr, c, a.n) : (int64_t)rr * a.y_stride + c));
+      const u32x2 r = resid;  // unit u == tid
       const u32 h0 = pack_bf16x2(bf16_lo(r[0]) + round_bf16(v[0][0]), bf16_hi(r[0]) + round_bf16(v[0][1]));
       const u32 h1 = pack_bf16x2(bf16_lo(r[1]) + round_bf16(v[0][2]), bf16_hi(r[1]) + round_bf16(v[0][3]));
       float ss = bf16_lo(h0) * bf16_lo(h0) + bf16_hi(h0) * bf16_hi(h0) + bf16_lo(h1) * bf16_lo(h1) +
