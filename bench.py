@@ -288,11 +288,13 @@ def small_decode_leg(args, device) -> dict:
     }
 
 
-# Larger decode shapes for the same kernel: batch and context ranges of the 32-sequence step at twice
-# the batch, at the load workload's context range (2048 prompt tokens + up to 2048 generated), and at
-# that workload's batch of 100.  Each shape rotates over `layers` pools whose summed read set is far
-# beyond the 256 MB Infinity Cache.
-SCALING_SHAPES = ((64, 256, 2304, 14), (32, 2048, 4096, 10), (100, 2048, 4096, 4))
+# Other decode shapes for the same kernel: the 32-sequence step at twice the batch, at the load
+# workload's context range (2048 prompt tokens + up to 2048 generated) and at that workload's batch
+# of 100; and one rank's share of the 32-sequence step under 8-way head parallelism (2 query heads,
+# 1 kv head).  Each shape rotates over `layers` pools whose summed read set is far beyond the 256 MB
+# Infinity Cache.  (batch, context lo, context hi, layers, query heads, kv heads)
+SCALING_SHAPES = ((64, 256, 2304, 14, 16, 8), (32, 2048, 4096, 10, 16, 8), (100, 2048, 4096, 4, 16, 8),
+                  (32, 256, 2304, 28, 2, 1))
 
 
 def decode_scaling_leg(args, device) -> list[dict]:
@@ -305,13 +307,14 @@ def decode_scaling_leg(args, device) -> list[dict]:
     from nano_vllm_ascend_amd import workloads as W
 
     rows = []
-    for batch, lo, hi, layers in SCALING_SHAPES:
-        work = W.make_decode(batch, lo, hi, batch * -(-hi // W.BLOCK_SIZE) + 8, args.seed, device, num_layers=layers)
+    for batch, lo, hi, layers, hq, hkv in SCALING_SHAPES:
+        work = W.make_decode(batch, lo, hi, batch * -(-hi // W.BLOCK_SIZE) + 8, args.seed, device, num_layers=layers,
+                             num_heads=hq, num_kv_heads=hkv)
         max_ctx = max(work.context_lens_list)
-        ws = _C.alloc_paged_decode_workspace(batch, W.NUM_HEADS, W.NUM_KV_HEADS, max_ctx, device)
+        ws = _C.alloc_paged_decode_workspace(batch, hq, hkv, max_ctx, device)
         out = torch.empty_like(work.q)
-        nbytes = (sum(work.context_lens_list) * W.NUM_KV_HEADS * W.HEAD_DIM * 2 * 2
-                  + 2 * batch * W.NUM_HEADS * W.HEAD_DIM * 2 + batch * work.block_tables.shape[1] * 4 + batch * 4)
+        nbytes = (sum(work.context_lens_list) * hkv * W.HEAD_DIM * 2 * 2
+                  + 2 * batch * hq * W.HEAD_DIM * 2 + batch * work.block_tables.shape[1] * 4 + batch * 4)
         scale = W.HEAD_DIM ** -0.5
 
         def step():
@@ -332,7 +335,7 @@ def decode_scaling_leg(args, device) -> list[dict]:
         us = start.elapsed_time(end) * 1e3 / (reps * layers)
         gbs = nbytes / us / 1e3
         rows.append({"workload": f"decode {batch} seqs, context U[{lo}, {hi}] (sum {sum(work.context_lens_list)}), "
-                                 f"{layers} layer pools",
+                                 f"{hq} q / {hkv} kv heads, {layers} layer pools",
                      "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3), "gbs": round(gbs, 1),
                      "frac": round(gbs / HBM_PEAK_GBS, 4)})
         del work, ws, out
