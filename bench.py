@@ -298,8 +298,8 @@ SCALING_SHAPES = ((64, 256, 2304, 14, 16, 8), (32, 2048, 4096, 10, 16, 8), (100,
 
 
 def decode_scaling_leg(args, device) -> list[dict]:
-    """GB/s of the decode kernel at the larger shapes (average over launches, HIP events on the
-    launch stream, as for `value`): how much of the 32-sequence step's gap to the HBM peak is the
+    """GB/s of the decode kernel at other shapes (average over the launches of graph replays, HIP
+    events on the launch stream): how much of the 32-sequence step's gap to the HBM peak is the
     launch's fixed ramp and merge tail, which larger launches amortise."""
     import torch
 
@@ -322,14 +322,22 @@ def decode_scaling_leg(args, device) -> list[dict]:
                 _C.paged_decode(out, work.q, work.key_cache[layer], work.value_cache[layer], work.block_tables,
                                 work.context_lens, scale, max_ctx, ws)
 
+        # replayed as one graph: the one-kv-head share's launches are shorter than a host-side
+        # launch, which would otherwise set their pace
         for _ in range(3):
             step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(3):
+            graph.replay()
         torch.cuda.synchronize()
         reps = max(5, args.steps * NUM_LAYERS // layers)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(reps):
-            step()
+            graph.replay()
         end.record()
         torch.cuda.synchronize()
         us = start.elapsed_time(end) * 1e3 / (reps * layers)

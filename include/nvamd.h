@@ -83,7 +83,7 @@ int nvamd_paged_decode(void *out, int64_t out_stride,
 /* ends, serves as the workspace.  A call that would need more returns      */
 /* NVAMD_ETOOLARGE and launches nothing (the need is                        */
 /* nvamd_paged_decode_workspace_size(batch, ...); 64 MiB covers e.g. 100    */
-/* sequences x 4096 tokens or 32 x 8192 at 16 query / 8 KV heads).  The     */
+/* sequences x 16384 tokens or 32 x 32768 at 16 query / 8 KV heads).  The   */
 /* first call on a device also clears the array's counters on `stream`.     */
 /* All calls on one GPU share its array: calls that overlap on one GPU race. */
 #define NVAMD_DECODE_SCRATCH_BYTES (64u * 1024u * 1024u)

@@ -57,7 +57,7 @@ constexpr int kPartFloats = 132;  // max, sum, 128 accumulators, 2 pad (16-byte 
 // results where another call expects a zero counter.
 constexpr int kCounterSlots = 16384;
 constexpr size_t kCounterBytes = kCounterSlots * sizeof(int);
-constexpr int kMinPart = 64;  // smallest partition any launch uses (sizes the workspace)
+constexpr int kMinPart = 256;  // smallest partition of a split launch (sizes the workspace)
 
 struct DecodeArgs {
   u16 *out;
@@ -600,8 +600,9 @@ int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
   // 256-token partitions of 4 waves (measured best on MI355X for 32 x ~1.3k contexts).  A launch
   // whose context bound gives fewer than two such items per CU is latency-bound: with a bound of
   // <= 1024 tokens one workgroup of bound/64 waves takes a whole (sequence, kv head), so there is
-  // no cross-workgroup merge; with longer bounds 128- or 64-token partitions of 2 or 1 waves
-  // spread the work over more CUs.
+  // no cross-workgroup merge.  Longer bounds keep the 256-token partitions at any batch: 128- or
+  // 64-token partitions of 2 or 1 waves (more workgroups, more partials to merge) measured
+  // 1.1-1.7x slower for 1-8 sequences of 2-4k tokens and for 32 sequences at one kv head.
   const int64_t units = (int64_t)batch * a.num_kv_heads;
   const int64_t want = 2LL * num_cus();
   if (units * ceil_div(a.max_ctx, 256) < want) {
@@ -611,10 +612,6 @@ int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
     if (nw_whole <= 8) return launch<GQA, 8, 1, 4, true, FUSED>(a, batch, stream);
     if constexpr (GQA <= 2) {  // 16 waves = 4 per SIMD: fits the 128 VGPRs of GQA <= 2
       if (nw_whole <= 16) return launch<GQA, 16, 1, 4, true, FUSED>(a, batch, stream);
-    }
-    if (ceil_div(a.max_ctx, 64) <= 64) {
-      if (units * ceil_div(a.max_ctx, 128) >= want) return launch<GQA, 2, 1, 4, false, FUSED>(a, batch, stream);
-      return launch<GQA, 1, 1, 4, false, FUSED>(a, batch, stream);
     }
   }
   int cpw = 1;

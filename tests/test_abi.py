@@ -116,5 +116,5 @@ def test_noalloc_decode_size_limit_is_checked_on_the_host():
     args = [A, 2048, A, 2048, A, A, 64, 128, A, 8, 8, A, 4, 16, 8, 128, 128 ** -0.5]
     assert lib.nvamd_paged_decode_noalloc(*args, 2_621_440, None) == ETOOLARGE
     assert lib.nvamd_paged_decode_noalloc(*args[:12], 0, *args[13:], 1024, None) == 0  # empty batch
-    fits = _C.paged_decode_workspace_size(100, 16, 8, 4096)
-    assert fits <= _C.DECODE_SCRATCH_BYTES < _C.paged_decode_workspace_size(100, 16, 8, 8192)
+    fits = _C.paged_decode_workspace_size(100, 16, 8, 16384)
+    assert fits <= _C.DECODE_SCRATCH_BYTES < _C.paged_decode_workspace_size(100, 16, 8, 32768)

@@ -49,7 +49,7 @@ def test_noalloc_decode_equals_workspace_decode_on_two_calls(device):
 @pytest.mark.gpu
 def test_noalloc_decode_refuses_sizes_beyond_the_scratch(device):
     work = W.make_decode(4, 1, 512, 64, seed=5, device=device)
-    bound = 2_621_440  # 4 rows x 8 kv heads x 2 GQA rows of partials per 64 tokens: 1.3 GB > 64 MiB
+    bound = 2_621_440  # 4 rows x 8 kv heads x 2 GQA rows of partials per 256 tokens: 346 MB > 64 MiB
     assert _C.paged_decode_workspace_size(4, 16, 8, bound) > _C.DECODE_SCRATCH_BYTES
     out = torch.zeros_like(work.q)
     with pytest.raises(ValueError, match="static scratch"):
