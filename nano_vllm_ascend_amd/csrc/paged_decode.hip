@@ -599,10 +599,12 @@ template <int GQA, bool FUSED>
 int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
   // 256-token partitions of 4 waves (measured best on MI355X for 32 x ~1.3k contexts).  A launch
   // whose context bound gives fewer than two such items per CU is latency-bound: with a bound of
-  // <= 1024 tokens one workgroup of bound/64 waves takes a whole (sequence, kv head), so there is
-  // no cross-workgroup merge.  Longer bounds keep the 256-token partitions at any batch: 128- or
-  // 64-token partitions of 2 or 1 waves (more workgroups, more partials to merge) measured
-  // 1.1-1.7x slower for 1-8 sequences of 2-4k tokens and for 32 sequences at one kv head.
+  // <= 512 tokens one workgroup of bound/64 waves takes a whole (sequence, kv head), so there is
+  // no cross-workgroup merge.  Beyond that one CU would stream a whole unit, and a CU alone reads
+  // at most ~41-57 GB/s: bounds of 513-1024 tokens split into 256-token partitions too (whole
+  // units of 16 waves measured 1.2-1.7x slower for 1-16 sequences).  The 256-token partitions
+  // stay at any batch: 128- or 64-token partitions of 2 or 1 waves (more workgroups, more partials
+  // to merge) measured 1.1-1.7x slower for 1-8 sequences of 2-4k tokens and for one kv head.
   const int64_t units = (int64_t)batch * a.num_kv_heads;
   const int64_t want = 2LL * num_cus();
   if (units * ceil_div(a.max_ctx, 256) < want) {
@@ -610,9 +612,6 @@ int dispatch(const DecodeArgs &a, int batch, hipStream_t stream) {
     if (nw_whole <= 2) return launch<GQA, 2, 1, 4, true, FUSED>(a, batch, stream);
     if (nw_whole <= 4) return launch<GQA, 4, 1, 4, true, FUSED>(a, batch, stream);
     if (nw_whole <= 8) return launch<GQA, 8, 1, 4, true, FUSED>(a, batch, stream);
-    if constexpr (GQA <= 2) {  // 16 waves = 4 per SIMD: fits the 128 VGPRs of GQA <= 2
-      if (nw_whole <= 16) return launch<GQA, 16, 1, 4, true, FUSED>(a, batch, stream);
-    }
   }
   int cpw = 1;
   while (ceil_div(a.max_ctx, 256 * cpw) > 64) cpw *= 2;
