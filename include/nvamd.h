@@ -242,7 +242,7 @@ int nvamd_pack_batch(const int32_t *desc, int batch,
 /*   is NULL), then out[r] = residual[r] * rsqrt(mean(residual[r]^2) + eps)   */
 /*   * weight, fp32 math, one bf16 rounding.  The decoder layer's residual    */
 /*   add + RMSNorm (nv/models/qwen3.py:138-150; npu_rms_norm at               */
-/*   nv/layers/layernorm.py:12-17).  hidden: a multiple of 1024, <= 4096.    */
+/*   nv/layers/layernorm.py:12-17).  hidden: any multiple of 8.              */
 /* silu_mul: out[r, i] = bf16(bf16(silu(gu[r, i])) * gu[r, inter + i]) for the */
 /*   fused gate/up projection (nv/models/qwen3.py:34-35).                     */
 /* argmax_rows: out[r] = first index of the maximum of logits[r, 0:vocab]     */

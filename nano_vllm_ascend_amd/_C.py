@@ -480,7 +480,8 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Tensor, v
 
 def add_rms_norm(delta: torch.Tensor | None, residual: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
                  eps: float) -> torch.Tensor:
-    """residual += delta (if given); out = RMSNorm(residual) * weight.  Rows of 1024k bf16 elements."""
+    """residual += delta (if given); out = RMSNorm(residual) * weight.  Rows of any multiple of 8 bf16
+    elements."""
     lib = load()
     _bf16_cuda("residual", residual)
     _bf16_cuda("out", out)

@@ -71,6 +71,51 @@ add_rms_norm_kernel(const u16 *__restrict__ delta, u16 *__restrict__ residual, c
   }
 }
 
+// Hidden sizes the kernel above does not take (any multiple of 8: Qwen3-4B's 2560, -14B's and
+// -32B's 5120).  One wave per row; lane l takes the 16-byte vectors l, l + 64, ...  The first pass
+// only sums the squares of the (added) row; the second reads the inputs again (L2 hits), forms
+// the same bf16 sums, and writes the residual and the normalised row.  Same rounding as above.
+template <bool ADD>
+__global__ void __launch_bounds__(256)
+add_rms_norm_any_kernel(const u16 *__restrict__ delta, u16 *__restrict__ residual, const u16 *__restrict__ weight,
+                        u16 *__restrict__ out, int rows, int hidden, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t base = (int64_t)row * hidden;
+  const int vecs = hidden / 8;
+  auto row_vec = [&](int i) {
+    u32x4 x = ld16(residual + base + 8 * i);
+    if (ADD) {
+      const u32x4 d = ld16(delta + base + 8 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = pack_bf16x2(bf16_lo(x[e]) + bf16_lo(d[e]), bf16_hi(x[e]) + bf16_hi(d[e]));
+    }
+    return x;
+  };
+  float ss = 0.f;
+  for (int i = lane; i < vecs; i += 64) {
+    const u32x4 x = row_vec(i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = bf16_lo(x[e]), b = bf16_hi(x[e]);
+      ss += a * a + b * b;
+    }
+  }
+  ss = wave_sum(ss);
+  const float rstd = rsqrtf(ss / (float)hidden + eps);
+  for (int i = lane; i < vecs; i += 64) {
+    const u32x4 x = row_vec(i);
+    if (ADD) st16(residual + base + 8 * i, x);
+    const u32x4 w = ld16(weight + 8 * i);
+    u32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      y[e] = pack_bf16x2(bf16_lo(x[e]) * rstd * bf16_lo(w[e]), bf16_hi(x[e]) * rstd * bf16_hi(w[e]));
+    st16(out + base + 8 * i, y);
+  }
+}
+
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
 // One thread per 8 output elements.
@@ -202,10 +247,21 @@ extern "C" int nvamd_add_rms_norm(const void *delta, void *residual, const void 
                                   int hidden, float eps, hipStream_t stream) {
   if (rows == 0) return NVAMD_OK;
   if (!residual || !weight || !out || rows < 0) return NVAMD_EINVAL;
-  if (hidden % 1024 != 0 || hidden > 4096 || hidden <= 0) return NVAMD_EUNSUPPORTED;
+  if (hidden <= 0 || hidden % 8 != 0) return NVAMD_EUNSUPPORTED;
   if (!aligned16(residual) || !aligned16(weight) || !aligned16(out) || (delta && !aligned16(delta)))
     return NVAMD_EINVAL;
   const dim3 grid((rows + 3) / 4);
+  if (hidden % 1024 != 0 || hidden > 4096) {
+    if (delta)
+      hipLaunchKernelGGL((add_rms_norm_any_kernel<true>), grid, dim3(256), 0, stream, static_cast<const u16 *>(delta),
+                         static_cast<u16 *>(residual), static_cast<const u16 *>(weight), static_cast<u16 *>(out), rows,
+                         hidden, eps);
+    else
+      hipLaunchKernelGGL((add_rms_norm_any_kernel<false>), grid, dim3(256), 0, stream, nullptr,
+                         static_cast<u16 *>(residual), static_cast<const u16 *>(weight), static_cast<u16 *>(out),
+                         rows, hidden, eps);
+    return launch_status();
+  }
   if (delta)
     hipLaunchKernelGGL((add_rms_norm_kernel<true>), grid, dim3(256), 0, stream, static_cast<const u16 *>(delta),
                        static_cast<u16 *>(residual), static_cast<const u16 *>(weight), static_cast<u16 *>(out), rows,

@@ -79,6 +79,10 @@ struct DecodeArgs {
   int max_ctx;
   int batch;
   float scale_log2e;
+  // Query heads of kv head g in q / out: q_group * g + q_head0 + (0 .. GQA-1).  One launch covers
+  // a whole group (q_group == GQA, q_head0 == 0) unless the ratio needs several launches.
+  int q_group;
+  int q_head0;
   // Fused decode step only: q holds the raw projection rows; the kernel applies the per-head
   // RMSNorm and RoPE to q and to the new token's k, and stores that k and the raw v at slots[b].
   const u16 *k_new;
@@ -93,6 +97,7 @@ struct DecodeArgs {
   int64_t num_slots;
   int max_positions;
   float eps;
+  bool store_new;  // this launch stores the new token's k / v (the first of a group's launches)
 };
 
 struct KVTile {
@@ -211,7 +216,7 @@ paged_decode_kernel(DecodeArgs a) {
   u32x4 qr[GQA][2];
 #pragma unroll
   for (int j = 0; j < GQA; ++j) {
-    const u16 *qp = a.q + (int64_t)b * a.q_stride + (int64_t)(g * GQA + j) * D + 8 * c;
+    const u16 *qp = a.q + (int64_t)b * a.q_stride + (int64_t)(g * a.q_group + a.q_head0 + j) * D + 8 * c;
     qr[j][0] = ld16(qp);
     qr[j][1] = ld16(qp + 64);
   }
@@ -267,7 +272,7 @@ paged_decode_kernel(DecodeArgs a) {
   };
   if constexpr (FUSED) {
     const bool nr_in = nr >= 0 && nr < ctx;
-    const bool owner = nr_in ? (nr >= t_begin && nr < t_end) : (p == n_parts - 1 && w == 0);
+    const bool owner = a.store_new && (nr_in ? (nr >= t_begin && nr < t_end) : (p == n_parts - 1 && w == 0));
     if (t_begin < t_end || owner) {
       const int64_t pc = nr < 0 ? 0 : (nr >= a.max_positions ? a.max_positions - 1 : nr);
       const float *row = a.cos_sin + pc * D + 8 * c;
@@ -471,7 +476,7 @@ paged_decode_kernel(DecodeArgs a) {
     mx[j] = M;
   }
 
-  u16 *out_base = a.out + (int64_t)b * a.out_stride + (int64_t)g * GQA * D + 2 * lane;
+  u16 *out_base = a.out + (int64_t)b * a.out_stride + (int64_t)(g * a.q_group + a.q_head0) * D + 2 * lane;
   if (n_parts <= 1) {
 #pragma unroll
     for (int j = 0; j < GQA; ++j) {
@@ -684,14 +689,24 @@ int fill_decode_args(DecodeArgs &a, void *out, int64_t out_stride, const void *q
   return NVAMD_OK;
 }
 
+// The kernel holds 1, 2 or 4 query heads per kv head in registers.  Other ratios (Qwen3-14B's 5,
+// Qwen3-32B's 8) run as consecutive launches over 4, then 2, then 1 heads of every group; each
+// re-reads the group's K/V, and only the first stores the fused step's new k / v.
 template <bool FUSED>
-int dispatch_gqa(const DecodeArgs &a, int gqa, int batch, hipStream_t stream) {
-  switch (gqa) {
-    case 1: return dispatch<1, FUSED>(a, batch, stream);
-    case 2: return dispatch<2, FUSED>(a, batch, stream);
-    case 4: return dispatch<4, FUSED>(a, batch, stream);
-    default: return NVAMD_EUNSUPPORTED;
+int dispatch_gqa(DecodeArgs a, int gqa, int batch, hipStream_t stream) {
+  a.q_group = gqa;
+  for (int head0 = 0; head0 < gqa;) {
+    const int rest = gqa - head0;
+    const int sub = rest >= 4 ? 4 : (rest >= 2 ? 2 : 1);
+    a.q_head0 = head0;
+    a.store_new = head0 == 0;
+    const int st = sub == 4 ? dispatch<4, FUSED>(a, batch, stream)
+                 : sub == 2 ? dispatch<2, FUSED>(a, batch, stream)
+                            : dispatch<1, FUSED>(a, batch, stream);
+    if (st != NVAMD_OK) return st;
+    head0 += sub;
   }
+  return NVAMD_OK;
 }
 
 }  // namespace

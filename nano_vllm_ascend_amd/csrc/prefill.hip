@@ -70,6 +70,10 @@ struct PrefillArgs {
   int num_kv_heads;
   int max_q_tiles;
   float scale_log2e;
+  // Query heads of kv head g in q / out: q_group * g + q_head0 + (0 .. GQA-1).  One launch covers
+  // a whole group (q_group == GQA, q_head0 == 0) unless the ratio needs several launches.
+  int q_group;
+  int q_head0;
 };
 
 // 16 bytes per lane into LDS at lds_base + 16 * lane (LDS-DMA), from a raw buffer (range
@@ -135,7 +139,7 @@ prefill_kernel(PrefillArgs a) {
   const int hl = lane >> 5;        // lane half
   const int n = lane & 31;         // this lane's query column
   const int j = w / WPH;           // head within the group
-  const int head = g * GQA + j;
+  const int head = g * a.q_group + a.q_head0 + j;
   const int r0 = qt * BQ + (w % WPH) * 32;  // first query row of this wave
   const int rq = r0 + n;
   const bool q_ok = rq < q_len;
@@ -388,14 +392,24 @@ int launch(const PrefillArgs &a, int n_seqs, hipStream_t stream) {
   return launch_status();
 }
 
+// A workgroup holds 1, 2 or 4 query heads of its kv head.  Other ratios (Qwen3-14B's 5, Qwen3-32B's
+// 8) run as consecutive launches over 4, then 2, then 1 heads of every group, each reading the
+// group's K/V again (the launches are compute-bound; the second read mostly hits the caches).
 template <bool PAGED>
 int dispatch(PrefillArgs a, int n_seqs, int gqa, int max_q_len, hipStream_t stream) {
-  switch (gqa) {
-    case 1: a.max_q_tiles = ceil_div(max_q_len, 32 * kWaves); return launch<1, PAGED>(a, n_seqs, stream);
-    case 2: a.max_q_tiles = ceil_div(max_q_len, 16 * kWaves); return launch<2, PAGED>(a, n_seqs, stream);
-    case 4: a.max_q_tiles = ceil_div(max_q_len, 8 * kWaves); return launch<4, PAGED>(a, n_seqs, stream);
-    default: return NVAMD_EUNSUPPORTED;
+  a.q_group = gqa;
+  for (int head0 = 0; head0 < gqa;) {
+    const int rest = gqa - head0;
+    const int sub = rest >= 4 ? 4 : (rest >= 2 ? 2 : 1);
+    a.q_head0 = head0;
+    a.max_q_tiles = ceil_div(max_q_len, 32 * kWaves / sub);
+    const int st = sub == 4 ? launch<4, PAGED>(a, n_seqs, stream)
+                 : sub == 2 ? launch<2, PAGED>(a, n_seqs, stream)
+                            : launch<1, PAGED>(a, n_seqs, stream);
+    if (st != NVAMD_OK) return st;
+    head0 += sub;
   }
+  return NVAMD_OK;
 }
 
 bool check_common(const void *out, int64_t out_stride, const void *q, int64_t q_stride, int num_heads,

@@ -66,6 +66,42 @@ def test_greedy_tokens_match_oracle_for_32_decode_steps(device):
     assert len(mismatches) <= total // 10
 
 
+# Other Qwen3 head layouts, 2 layers each: 40 query / 8 kv heads (Qwen3-14B's ratio 5) on the
+# 0.6B hidden size, which takes the fused decode path; 32 / 4 heads (ratio 8) on Qwen3-4B's hidden
+# and MLP sizes, which takes the unfused one.  Both run attention as several launches per layer.
+WIDE_GQA = {
+    "gqa5_fused": replace(QWEN3_0_6B, num_hidden_layers=2, num_attention_heads=40, num_key_value_heads=8),
+    "gqa8_unfused": replace(QWEN3_0_6B, num_hidden_layers=2, num_attention_heads=32, num_key_value_heads=4,
+                            hidden_size=2560, intermediate_size=9728),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(WIDE_GQA))
+def test_other_gqa_ratios_match_oracle(device, name):
+    cfg = WIDE_GQA[name]
+    llm = make_llm(layers=cfg)
+    llm.runner.tokenizer.eos_token_id = -1
+    fused = llm.runner.model.decode_fusable(2)
+    assert fused == (name == "gqa5_fused")
+    prompts = prompts_for([37, 150], seed=5)
+    outs = llm.generate(prompts, max_new_tokens=17)
+    state = {k: v for k, v in llm.runner.model.state_dict().items()}
+    mismatches, total = [], 0
+    for prompt, out in zip(prompts, outs):
+        ref = Qwen3Ref(state, cfg, round_bf16=True, max_positions=512)
+        logits = ref.forward(prompt)
+        for step, tok in enumerate(out["token_ids"]):
+            top = int(logits.argmax())
+            total += 1
+            if top != tok:
+                mismatches.append((step, float(logits[top] - logits[tok])))
+            logits = ref.forward([tok])
+    print(f"{name}: {total - len(mismatches)}/{total} tokens equal; mismatches (step, margin) {mismatches}")
+    assert all(m < TIE_TOL for _, m in mismatches), mismatches
+    assert len(mismatches) <= total // 10
+
+
 @pytest.mark.gpu
 def test_decode_logits_match_oracle_each_step(device):
     llm = make_llm()

@@ -105,7 +105,8 @@ def test_fused_step_batch4_whole_units(device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("heads,bs", [((8, 8), 16), ((16, 4), 64), ((16, 8), 32)])
+@pytest.mark.parametrize("heads,bs", [((8, 8), 16), ((16, 4), 64), ((16, 8), 32), ((40, 8), 128), ((32, 4), 16),
+                                      ((24, 8), 64)])
 def test_fused_step_gqa_and_block_sizes(device, heads, bs):
     check(Case(device, 24, 40, 1500, 4096 if bs <= 32 else 1024, seed=2, heads=heads, bs=bs))
 

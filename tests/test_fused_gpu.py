@@ -13,7 +13,9 @@ def _bf(shape, gen, device, scale=1.0):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows,hidden", [(1, 1024), (33, 1024), (5, 2048), (7, 4096)])
+# 2560 (Qwen3-4B), 5120 (-14B / -32B), 8200 and 8: the any-width kernel
+@pytest.mark.parametrize("rows,hidden", [(1, 1024), (33, 1024), (5, 2048), (7, 4096), (9, 2560), (6, 5120),
+                                         (3, 8200), (70, 8)])
 def test_add_rms_norm_matches_reference_rounding(device, rows, hidden):
     g = torch.Generator(device=device).manual_seed(rows)
     res = _bf((rows, hidden), g, device)

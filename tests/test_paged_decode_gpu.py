@@ -104,8 +104,13 @@ def test_decode_large_ragged_batch_with_empty_sequences(device):
     assert (out_tight.float().cpu() - ref).abs().max().item() <= TOL
 
 
+# (24, 8), (40, 8) and (32, 4): ratios 3, 5 and 8 (Qwen3-14B and -32B have 5 and 8) run as several
+# launches over 4, 2 and 1 query heads of every kv head.
+GQA_HEADS = [(8, 8), (16, 8), (16, 4), (24, 8), (40, 8), (32, 4)]
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("heads", [(8, 8), (16, 8), (16, 4)])
+@pytest.mark.parametrize("heads", GQA_HEADS)
 def test_decode_gqa_groups(device, heads):
     hq, hkv = heads
     work = W.make_decode(5, 1, 700, 64, seed=7, device=device, num_heads=hq, num_kv_heads=hkv)
@@ -120,7 +125,7 @@ def test_decode_block_sizes(device, bs):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("heads", [(8, 8), (16, 8), (16, 4)])
+@pytest.mark.parametrize("heads", GQA_HEADS)
 @pytest.mark.parametrize("bs", [16, 128])
 def test_decode_split_path_gqa_and_block_sizes(device, heads, bs):
     """Batches large enough for the split-KV launch (nontemporal loads, cross-workgroup merge)

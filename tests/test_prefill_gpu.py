@@ -44,7 +44,7 @@ def test_dense_prefill_edge_lengths(device, lens):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("heads", [(8, 8), (16, 4)])
+@pytest.mark.parametrize("heads", [(8, 8), (16, 4), (24, 8), (40, 8), (32, 4)])  # ratios 1, 4, 3, 5, 8
 def test_dense_prefill_gqa_groups(device, heads):
     out, q, k, v, cu = run_dense([33, 200, 129], heads[0], heads[1], device, seed=4)
     ref = varlen_prefill_ref(q, k, v, cu, SCALE)
@@ -148,6 +148,17 @@ def test_paged_prefix_hit_prefill(device, bs):
                       SCALE)
     torch.cuda.synchronize()
     assert (out.float() - dense[sel].float()).abs().max().item() <= TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads", [(40, 8), (32, 4)])
+def test_paged_prefill_gqa_launch_groups(device, heads):
+    """Ratios 5 and 8 run as several launches over 4, 2 and 1 query heads of every kv head."""
+    prompt_lens, cached = [300, 129, 700], [256, 0, 384]
+    out, qs, q, k, v, kc, vc, tables, cu_q, cu_full, sel = _paged_case(device, prompt_lens, cached, bs=64, seed=9,
+                                                                       hq=heads[0], hkv=heads[1])
+    ref = paged_prefill_ref(qs, kc, vc, tables, cu_q, prompt_lens, SCALE)
+    assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
 @pytest.mark.gpu
