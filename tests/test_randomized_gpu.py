@@ -18,6 +18,8 @@ from nano_vllm_ascend_amd import _C
 from nano_vllm_ascend_amd import workloads as W
 from oracle.attention_ref import paged_decode_ref, paged_prefill_ref, varlen_prefill_ref
 
+from test_fused_decode_gpu import Case, check as check_fused
+
 TOL = 2e-2
 SCALE = W.HEAD_DIM ** -0.5
 HEADS = [(8, 8), (16, 8), (24, 8), (16, 4), (40, 8), (32, 4), (4, 1)]
@@ -116,3 +118,19 @@ def test_random_prefill_shapes(device, seed):
     refp = paged_prefill_ref(qs, kc, vc, tables, cu_q, lens, SCALE)
     errp = (outp.float().cpu() - refp).abs().max().item()
     assert errp <= TOL, (lens, cached, bs, hq, hkv, errp)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(6))
+def test_random_fused_decode_steps(device, seed):
+    """The fused decode step (norm, RoPE, KV store, attention in one launch per query-head group)
+    equals the two-launch chain bit for bit and the oracle within the tolerance, on random shapes."""
+    rng = random.Random(2000 + seed)
+    batch = rng.choice([2, 9, 40])
+    heads = rng.choice(HEADS)
+    bs = rng.choice([16, 64, 128])
+    ctx = _lengths(rng, batch, rng.choice([500, 2500]))
+    print(f"fused case {seed}: batch {batch}, heads {heads}, block {bs}, contexts up to {max(ctx)}", flush=True)
+    num_blocks = sum(math.ceil(c / bs) for c in ctx) + 4
+    check_fused(Case(device, batch, 0, 0, num_blocks, seed=seed, heads=heads, bs=bs, context_lens=ctx),
+                max_ctx=max(ctx) + rng.choice([0, 100]))
