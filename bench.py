@@ -229,7 +229,7 @@ def fused_step_leg(args, work, device) -> dict:
     return {"workload": "decode step, 32 seqs, context U[256, 2304]: q/k norm + RoPE + KV store + attention",
             "two_launches_us_per_layer": round(two, 3), "fused_us_per_layer": round(one, 3),
             "saved_us_per_layer": round(two - one, 3), "bytes": step_bytes,
-            "fused_gbs": round(step_bytes / one / 1e3, 1)}
+            "fused_gbs": round(step_bytes / one / 1e3, 1), "fused_frac": round(step_bytes / one / 1e3 / HBM_PEAK_GBS, 4)}
 
 
 def small_decode_leg(args, device) -> dict:
