@@ -220,6 +220,46 @@ def test_qwen3_oracle_fp32_matches_hf_model():
     assert torch.allclose(logits2, hf_logits[-1], atol=1e-4)
 
 
+def test_qwen3_oracle_batched_and_fp64_modes_agree_with_single_sequence_fp32():
+    """forward_batch runs each sequence on its own cache: row i equals the single-sequence forward of
+    sequence i (fp32, to summation order); fp64 arithmetic agrees with fp32 to fp32 rounding."""
+    cfg = _tiny_config()
+    state = _tiny_state(cfg, seed=2)
+    prompts = [[5, 77, 300, 12], [9, 480, 1, 33], [7, 7, 7, 7]]
+    nxt = [[40], [41], [42]]
+    single = []
+    for p, n in zip(prompts, nxt):
+        ref = Qwen3Ref(state, cfg, round_bf16=False, max_positions=64)
+        single.append((ref.forward(p), ref.forward(n)))
+    for dtype in (torch.float32, torch.float64):
+        batch = Qwen3Ref(state, cfg, round_bf16=False, max_positions=64, dtype=dtype)
+        batch.reset(len(prompts))
+        first, second = batch.forward_batch(prompts), batch.forward_batch(nxt)
+        for i, (a, b) in enumerate(single):
+            assert torch.allclose(first[i], a, atol=2e-5) and torch.allclose(second[i], b, atol=2e-5), (dtype, i)
+    # the sequences must not see each other: a different second prompt leaves row 0 unchanged
+    other = Qwen3Ref(state, cfg, round_bf16=False, max_positions=64)
+    other.reset(2)
+    assert torch.allclose(other.forward_batch([prompts[0], prompts[1][::-1]])[0], single[0][0], atol=2e-5)
+    with pytest.raises(ValueError):
+        other.forward_batch([[1, 2], [3]])
+
+
+def test_qwen3_oracle_bf16_logits_and_rounded_probabilities():
+    """bf16 mode returns logits the reference's bf16 LM head can produce (exact bf16 values); rounding
+    softmax probabilities to bf16 changes nothing where every probability is 1 (one key: the first
+    token) and changes the logits by rounding only elsewhere."""
+    cfg = _tiny_config()
+    state = _tiny_state(cfg, seed=3)
+    plain = Qwen3Ref(state, cfg, round_bf16=True, max_positions=64)
+    probs = Qwen3Ref(state, cfg, round_bf16=True, max_positions=64, round_probs=True)
+    a, b = plain.forward([11]), probs.forward([11])
+    assert torch.equal(a, a.to(torch.bfloat16).float())
+    assert torch.equal(a, b)  # softmax over one key is exactly 1.0 in both
+    a, b = plain.forward([12, 13, 14]), probs.forward([12, 13, 14])
+    assert 0 < (a - b).abs().max().item() < 0.1
+
+
 # --- planted mistakes: plausible bugs that the pins above must catch ---
 def test_planted_gqa_mapping_error_is_caught(monkeypatch):
     def wrong_attend(q, k, v, scale, allowed):  # kv head h % Hkv instead of h // group
