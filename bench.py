@@ -223,9 +223,11 @@ def fused_step_leg(args, work, device) -> dict:
 
     two = us_per_layer(two_launches)
     one = us_per_layer(fused)
-    # algorithmic bytes of the step: the attention's, plus raw q/k/v read, the new k/v stored
+    # algorithmic bytes of the step: the attention's (K/V, raw q read once, out written, table row, context
+    # length), plus per sequence the raw new k and v read, the new k/v stored, position and slot, and the
+    # fp32 cos/sin row; and the two norm weights once
     step_bytes = (sum(work.context_lens_list) * hkv * d * 2 * 2 + 2 * b * hq * d * 2 + b * work.block_tables.shape[1] * 4
-                  + b * 4 + b * ((hq + hkv) * d * 2 + hkv * d * 2 + 2 * hkv * d * 2 + 16))
+                  + b * 4 + b * (2 * hkv * d * 2 + 2 * hkv * d * 2 + 16 + d * 4) + 2 * d * 2)
     return {"workload": "decode step, 32 seqs, context U[256, 2304]: q/k norm + RoPE + KV store + attention",
             "two_launches_us_per_layer": round(two, 3), "fused_us_per_layer": round(one, 3),
             "saved_us_per_layer": round(two - one, 3), "bytes": step_bytes,

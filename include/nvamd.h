@@ -36,6 +36,8 @@ extern "C" {
 #define NVAMD_EUNSUPPORTED (-2) /* head_dim / GQA group / block_size not built */
 #define NVAMD_EWORKSPACE (-3)  /* workspace missing or too small               */
 #define NVAMD_ETOOLARGE (-4)   /* needs more than the library's static scratch  */
+#define NVAMD_ECAPTURE (-5)    /* first use of the static scratch on a device   */
+                               /* made while `stream` is being captured         */
 
 /* ABI version of this header; nvamd_version() returns the version the library was built
    with, for the loader's sanity check. */
@@ -84,7 +86,10 @@ int nvamd_paged_decode(void *out, int64_t out_stride,
 /* NVAMD_ETOOLARGE and launches nothing (the need is                        */
 /* nvamd_paged_decode_workspace_size(batch, ...); 64 MiB covers e.g. 100    */
 /* sequences x 16384 tokens or 32 x 32768 at 16 query / 8 KV heads).  The   */
-/* first call on a device also clears the array's counters on `stream`.     */
+/* first call on a device also clears the array's counters on `stream`, so */
+/* it must not be made while `stream` is captured into a graph (the clear  */
+/* would only be recorded): it then returns NVAMD_ECAPTURE and launches     */
+/* nothing.  Once one call has run outside capture, calls may be captured.  */
 /* All calls on one GPU share its array: calls that overlap on one GPU race. */
 #define NVAMD_DECODE_SCRATCH_BYTES (64u * 1024u * 1024u)
 int nvamd_paged_decode_noalloc(void *out, int64_t out_stride,
@@ -280,7 +285,8 @@ int nvamd_argmax_rows(const void *logits, int64_t row_stride, int rows,
 /*   rows past m are neither read as inputs nor written).                     */
 /* Prologue: with x_ssq == NULL, a = x.  Otherwise x is the residual stream,  */
 /*   x_ssq[r * (k/32) + t] holds the sum of squares of x[r, 32t..32t+31], and */
-/*   a = bf16((x * rsqrt(sum_t x_ssq / k + eps)) * norm_weight); k <= 4096.  */
+/*   a = bf16((x * rsqrt(sum_t x_ssq / k + eps)) * norm_weight); k <= 2048   */
+/*   (NVAMD_EUNSUPPORTED above).                                              */
 /* epilogue 0 (store): y[r, c] = bf16(acc).                                   */
 /* epilogue 1 (silu_mul): w is the fused [2n, k] gate/up weight;              */
 /*   y[r, c] = bf16(bf16(silu(bf16(acc_gate))) * bf16(acc_up)).               */

@@ -18,7 +18,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libnvamd.so"
 
 NVAMD_OK = 0
 _ERRORS = {-1: "invalid argument", -2: "unsupported configuration", -3: "workspace missing or too small",
-           -4: "needs more than the library's static scratch (NVAMD_DECODE_SCRATCH_BYTES)"}
+           -4: "needs more than the library's static scratch (NVAMD_DECODE_SCRATCH_BYTES)",
+           -5: "first use of the static scratch on this device made while the stream is captured; make one "
+               "call outside graph capture first"}
 DECODE_SCRATCH_BYTES = 64 * 1024 * 1024  # NVAMD_DECODE_SCRATCH_BYTES
 
 _c_int = ctypes.c_int
@@ -248,8 +250,9 @@ def paged_decode_noalloc(out: torch.Tensor, q: torch.Tensor, key_cache: torch.Te
     """``paged_decode`` without a workspace: the library's static per-GPU scratch serves as one.
 
     Raises ValueError when the call needs more than DECODE_SCRATCH_BYTES
-    (paged_decode_workspace_size of its sizes).  Calls that overlap on one GPU share the
-    scratch and race.
+    (paged_decode_workspace_size of its sizes), or when the first call on a device is made under
+    graph capture (the first call clears the scratch's counters, which capture would only record).
+    Calls that overlap on one GPU share the scratch and race.
     """
     lib = load()
     args = _decode_args(out, q, key_cache, value_cache, block_tables, context_lens, scale, max_context_len)

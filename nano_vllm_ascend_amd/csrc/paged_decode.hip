@@ -769,7 +769,8 @@ extern "C" int nvamd_paged_decode_fused(void *out, int64_t out_stride, const voi
 // name is only a host-side stand-in, never an address: the first call on a device, with that
 // device current, asks hipGetSymbolAddress for that device's copy, keeps the address per
 // device, and clears the copy's arrival counters with a fill kernel on the caller's stream
-// (ordered before the call's own launch).  Every call leaves the counters at zero again, as it
+// (ordered before the call's own launch); that first call is refused while the stream is being
+// captured, since the clear would only be recorded.  Every call leaves the counters at zero again, as it
 // does with a caller's workspace; partial results need no clearing.  Calls share the device's
 // copy: calls that can overlap on one GPU (several streams, several host threads) race on it.
 __device__ __align__(256) unsigned char scratch[NVAMD_DECODE_SCRATCH_BYTES];
@@ -794,6 +795,12 @@ int device_scratch(hipStream_t stream, void **ptr) {
   if (dev < 0 || dev >= kMaxDevices) return NVAMD_EUNSUPPORTED;
   std::lock_guard<std::mutex> guard(g_scratch_lock);
   if (g_scratch[dev] == nullptr) {
+    // The counter clear below must run now, not be recorded into a graph that may never replay
+    // before the next eager call.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(stream, &capture);
+    if (err != hipSuccess) return (int)err;
+    if (capture != hipStreamCaptureStatusNone) return NVAMD_ECAPTURE;
     void *p = nullptr;
     err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (err != hipSuccess) return (int)err;

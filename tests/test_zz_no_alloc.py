@@ -29,6 +29,47 @@ def _both(work, bound, device):
 
 
 @pytest.mark.gpu
+def test_noalloc_decode_captured_in_a_graph_equals_workspace_decode(device):
+    """Graph capture is what the entry point is for.  The first call on a device clears the scratch's
+    counters, so it is refused under capture (ValueError, nothing recorded); once a call ran eagerly,
+    a captured call replays correctly, with eager calls in between, and with new q values."""
+    work = W.decode_step(device, seed=6)
+    q, kc, vc = work.q, work.key_cache[0], work.value_cache[0]
+    got = torch.full_like(q, float("nan"))
+    args = (kc, vc, work.block_tables, work.context_lens, SCALE, 2304)
+    g = torch.cuda.CUDAGraph()
+    try:  # refused only if no call has set the device up yet (this test runs first in its file)
+        with torch.cuda.graph(g):
+            _C.paged_decode_noalloc(got, q, *args)
+        refused = False
+    except ValueError as e:
+        assert "graph capture" in str(e)
+        refused = True
+    print(f"[no-alloc] first capture refused: {refused}", flush=True)
+    torch.cuda.synchronize()
+    if refused:
+        _C.paged_decode_noalloc(got, q, *args)  # eager: sets the device up
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            _C.paged_decode_noalloc(got, q, *args)
+    ws = _C.alloc_paged_decode_workspace(q.shape[0], 16, 8, 2304, device)
+    for rep in range(3):
+        if rep == 2:
+            q.mul_(-0.5)  # the graph reads q in place
+        want = torch.empty_like(q)
+        _C.paged_decode(want, q, *args[:-1], 2304, ws)
+        got.fill_(float("nan"))
+        small = W.make_decode(4, 1, 512, 64, seed=rep, device=device)  # an eager call between replays
+        other = torch.empty_like(small.q)
+        _C.paged_decode_noalloc(other, small.q, small.key_cache[0], small.value_cache[0], small.block_tables,
+                                small.context_lens, SCALE, 4096)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), rep
+
+
+@pytest.mark.gpu
 def test_noalloc_decode_equals_workspace_decode_on_two_calls(device):
     # first: 32 sequences of U[256, 2304] (split-KV launches: the counters and partials are used)
     big = W.decode_step(device, seed=3)
