@@ -586,9 +586,9 @@ def cpu_baseline(work, seed: int, reps: int = 20):
     }
 
 
-def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 2) -> dict:
-    """fp32 oracle on the host cores for the other decode shape (median of 20 reps after 3
-    warm-ups) and for the ragged prefill (a bounded sample of `prefill_reps` reps)."""
+def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 20) -> dict:
+    """fp32 oracle on the host cores for the other decode shape, the ragged prefill and its KV write
+    (the reference's index_copy_ into the flattened cache), each a median of 20 reps after 3 warm-ups."""
     import torch
 
     from nano_vllm_ascend_amd import workloads as W
@@ -617,10 +617,32 @@ def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 2) -> dict:
     pk = torch.randn(t, 8, 128, generator=g).bfloat16()
     pv = torch.randn(t, 8, 128, generator=g).bfloat16()
     cu = torch.tensor(W.cu_seqlens(lens), dtype=torch.int32)
-    t0 = time.perf_counter()
-    for _ in range(prefill_reps):
-        varlen_prefill_ref(pq, pk, pv, cu, scale)
-    pf_s = (time.perf_counter() - t0) / prefill_reps
+
+    def median(fn, reps):
+        for _ in range(3):
+            fn()
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[reps // 2]
+
+    pf_s = median(lambda: varlen_prefill_ref(pq, pk, pv, cu, scale), prefill_reps)
+    # the prompts' K/V written into a 128-token-block cache through a seeded slot mapping, as
+    # PagedKVCache.write does (nv/npu/paged_kv_cache.py:68-69: index_copy_ along the flattened slots)
+    pool = W.seeded_block_tables(lens, 1024, 128, seed)
+    kv_slots = torch.tensor([int(pool.block_tables[i, p // 128]) * 128 + p % 128 for i, n in enumerate(lens)
+                             for p in range(n)], dtype=torch.int64)
+    kcache = torch.zeros(1024 * 128, 8, 128, dtype=torch.bfloat16)
+    vcache = torch.zeros_like(kcache)
+
+    def kv_write():
+        kcache.index_copy_(0, kv_slots, pk)
+        vcache.index_copy_(0, kv_slots, pv)
+
+    kv_s = median(kv_write, 20)
+    kv_bytes = 2 * 2 * t * 8 * 128 * 2 + t * 8  # K and V read and written, and the slot mapping
     # reference-style packing: the per-token slot loop on the host
     bm = BlockManagerRef(1024, 128)
     slots = list(range(32))
@@ -640,7 +662,12 @@ def cpu_baselines_other(small_work, seed: int, prefill_reps: int = 2) -> dict:
                                     "sample": "oracle block manager (per-token slot loop), median of 5"},
         "prefill_32xU64-2048": {"ms": round(pf_s * 1e3, 1),
                                 "tflops": round(W.causal_attention_flops(lens, lens, 16) / pf_s / 1e12, 3),
-                                "sample": f"fp32 torch-CPU oracle, {prefill_reps} reps (bounded sample)"},
+                                "sample": f"fp32 torch-CPU oracle, median of {prefill_reps} after 3 warm-ups"},
+        "kv_write_32xU64-2048": {"ms": round(kv_s * 1e3, 2), "bytes": kv_bytes,
+                                 "gbs": round(kv_bytes / kv_s / 1e9, 2),
+                                 "sample": "torch-CPU index_copy_ of the prompts' bf16 K and V into a 1024 x 128-token "
+                                           "block cache through the slot mapping (the reference's PagedKVCache.write), "
+                                           "median of 20 after 3 warm-ups"},
     }
 
 

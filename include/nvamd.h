@@ -41,8 +41,31 @@ extern "C" {
 
 /* ABI version of this header; nvamd_version() returns the version the library was built
    with, for the loader's sanity check. */
-#define NVAMD_ABI_VERSION 2
+#define NVAMD_ABI_VERSION 3
 int nvamd_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* Index errors.  Where the reference's indexing raises -- index_copy_ with a */
+/* slot outside the cache (nv/npu/paged_kv_cache.py:68-69), the RoPE cache    */
+/* indexed past its end (nv/layers/rotary_embedding.py:49-50), a context     */
+/* longer than its block-table row or the launch's bound, a block id outside */
+/* the pool (nv/layers/npu_paged_attention.py:89-99,                         */
+/* nv/layers/npu_prefill_attention.py:73-96) -- the kernels skip the write or */
+/* clamp the read, so no access leaves its buffer, and set the matching bit   */
+/* in a per-device error word (an atomic OR; nothing is done on the normal    */
+/* path).  A slot of -1 marks a padding row: skipped without an error.      */
+/* nvamd_errors_fetch enqueues a copy of the word into `host` (4 bytes;      */
+/* pinned memory keeps the copy asynchronous) on `stream`, so a caller reads  */
+/* it with the step's other results instead of synchronising per call;       */
+/* nvamd_errors_clear enqueues a kernel that zeroes it.  Both can be         */
+/* captured.  The word starts at zero when the library is loaded.            */
+/* Neither has a counterpart in the reference, which raises synchronously.   */
+#define NVAMD_ERR_SLOT 1u     /* slot_mapping entry < -1 or >= cache slots   */
+#define NVAMD_ERR_POSITION 2u /* position < 0 or >= the RoPE table's rows    */
+#define NVAMD_ERR_CONTEXT 4u  /* context < 0 or past its table row / bound   */
+#define NVAMD_ERR_BLOCK 8u    /* block-table entry < 0 or >= num_blocks      */
+int nvamd_errors_fetch(unsigned *host, hipStream_t stream);
+int nvamd_errors_clear(hipStream_t stream);
 
 /* ------------------------------------------------------------------------- */
 /* P4: GQA paged decode attention.                                            */

@@ -32,6 +32,8 @@ _c_float = ctypes.c_float
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "nvamd_version": (_c_int, []),
+    "nvamd_errors_fetch": (_c_int, [_c_ptr, _c_ptr]),
+    "nvamd_errors_clear": (_c_int, [_c_ptr]),
     "nvamd_paged_decode_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "nvamd_paged_decode": (
         _c_int,
@@ -159,6 +161,61 @@ def _bf16_cuda(name: str, t: torch.Tensor) -> None:
 
 def version() -> int:
     return int(load().nvamd_version())
+
+
+# ------------------------------------------------------------------ index errors (device error word)
+# Where the reference's indexing raises IndexError (index_copy_ into the KV cache, the RoPE cache
+# lookup, the block-table gather), the kernels skip or clamp the access and set a bit in a
+# per-device error word.  The runner copies the word to the host with each step's tokens (no extra
+# synchronisation) and raises IndexError there.
+ERR_SLOT, ERR_POSITION, ERR_CONTEXT, ERR_BLOCK = 1, 2, 4, 8  # NVAMD_ERR_*
+_ERR_TEXT = {
+    ERR_SLOT: "a slot_mapping entry outside the KV cache (index_copy_, nv/npu/paged_kv_cache.py:68-69)",
+    ERR_POSITION: "a position outside the RoPE table (nv/layers/rotary_embedding.py:49-50)",
+    ERR_CONTEXT: "a context length its block-table row or the launch's bound cannot hold",
+    ERR_BLOCK: "a block-table entry outside the block pool",
+}
+
+
+def describe_index_errors(bits: int) -> str:
+    parts = [text for bit, text in _ERR_TEXT.items() if bits & bit]
+    unknown = bits & ~sum(_ERR_TEXT)
+    if unknown:
+        parts.append(f"unknown bits {unknown:#x}")
+    return "; ".join(parts)
+
+
+def clear_index_errors() -> None:
+    """Zero the current device's error word (a kernel on the current stream)."""
+    _check(load().nvamd_errors_clear(_stream()), "nvamd_errors_clear")
+
+
+class IndexErrorWord:
+    """A host copy of the device's index-error word, fetched on the current stream beside a step's
+    other results (pinned memory, so the copy is asynchronous) and checked once they have landed."""
+
+    def __init__(self, host: torch.Tensor | None = None):
+        self.host = host if host is not None else torch.zeros(1, dtype=torch.int32, pin_memory=True)
+
+    def fetch(self) -> None:
+        _check(load().nvamd_errors_fetch(self.host.data_ptr(), _stream()), "nvamd_errors_fetch")
+
+    def raise_if_set(self) -> None:
+        """Call after the copy has landed (the step's tokens were read)."""
+        bits = int(self.host[0])
+        if bits:
+            self.host.zero_()
+            clear_index_errors()
+            raise IndexError(f"index out of range in the step's kernels: {describe_index_errors(bits)} "
+                             f"(error word {bits:#x})")
+
+
+def index_errors() -> int:
+    """The current device's error word, read synchronously (tests and debugging)."""
+    word = IndexErrorWord()
+    word.fetch()
+    torch.cuda.current_stream().synchronize()
+    return int(word.host[0])
 
 
 # ------------------------------------------------------------------ optional host-side range checks

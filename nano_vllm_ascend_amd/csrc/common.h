@@ -203,4 +203,13 @@ inline int launch_status() {
   return e == hipSuccess ? NVAMD_OK : (int)e;
 }
 
+// The current device's index-error word (errors.hip), or nullptr if it cannot be looked up (the
+// kernels then report nothing).  Kernels take it as an argument and OR NVAMD_ERR_* bits into it
+// where the reference's indexing would raise; on the normal path they never touch it.
+u32 *index_error_word();
+
+__device__ __forceinline__ void flag_index_error(u32 *word, u32 bit) {
+  if (word != nullptr) __hip_atomic_fetch_or(word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace nvamd

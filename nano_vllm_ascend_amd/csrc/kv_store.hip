@@ -6,7 +6,9 @@
 //   as composed in Qwen3Attention.forward (nv/models/qwen3.py:83-96).
 //
 // Both are pure HBM streams: every byte is read once and written once, with 16-byte
-// accesses (eight lanes cover one 256-byte head row in two 128-byte halves).
+// accesses (eight lanes cover one 256-byte head row in two 128-byte halves).  A slot past the
+// cache or a position past the RoPE table, where the reference's indexing raises, is skipped or
+// clamped and reported in the index-error word.
 #include "common.h"
 
 namespace nvamd {
@@ -16,14 +18,18 @@ namespace {
 __global__ void __launch_bounds__(256)
 kv_cache_write_kernel(const u16 *__restrict__ k, int64_t k_stride, const u16 *__restrict__ v, int64_t v_stride,
                       u16 *__restrict__ k_cache, u16 *__restrict__ v_cache, const int64_t *__restrict__ slots,
-                      int num_tokens, int num_kv_heads, int64_t num_slots) {
+                      int num_tokens, int num_kv_heads, int64_t num_slots, u32 *err) {
   const int chunks_per_token = num_kv_heads * (kHeadDim / 8);
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)num_tokens * chunks_per_token) return;
   const int t = (int)(i / chunks_per_token);
   const int ch = (int)(i % chunks_per_token);  // = head * 16 + chunk
   const int64_t slot = slots[t];
-  if (slot < 0 || slot >= num_slots) return;
+  if (slot >= num_slots || slot < -1) {  // index_copy_ would raise: skip the row, report it once per token
+    if (ch == 0) flag_index_error(err, NVAMD_ERR_SLOT);
+    return;
+  }
+  if (slot < 0) return;  // -1: a padding row
   const int64_t dst = slot * ((int64_t)num_kv_heads * kHeadDim) + (int64_t)ch * 8;
   // Nontemporal loads and stores: each byte is touched once.  Over 38k tokens, with consecutive
   // launches on different buffers (so no launch finds its bytes in the Infinity Cache), this runs
@@ -54,6 +60,7 @@ struct NormRopeArgs {
   int num_heads;
   int num_kv_heads;
   float eps;
+  u32 *err;  // index-error word
 };
 
 // An aligned group of 8 lanes owns one head vector of one token: lane c holds dims
@@ -75,7 +82,10 @@ qk_norm_rope_kernel(NormRopeArgs a) {
   int64_t slot = -1;
   if (store) {
     slot = a.slots[t];
-    if (slot >= a.num_slots) slot = -1;
+    if (slot >= a.num_slots || slot < -1) {  // index_copy_ would raise: skip the row, report it once per token
+      if (vec == 0 && c == 0) flag_index_error(a.err, NVAMD_ERR_SLOT);
+      slot = -1;
+    }
   }
   const int64_t cache_row = slot * ((int64_t)a.num_kv_heads * kHeadDim);
 
@@ -97,7 +107,10 @@ qk_norm_rope_kernel(NormRopeArgs a) {
   u32x4 lo = ld16(x), hi = ld16(x + 64);
   const u32x4 w_lo = ld16(wt), w_hi = ld16(wt + 64);
   int64_t pos = a.positions[t];
-  pos = pos < 0 ? 0 : (pos >= a.max_positions ? a.max_positions - 1 : pos);
+  if (pos < 0 || pos >= a.max_positions) {  // the RoPE cache lookup would raise: clamp and report
+    if (vec == 0 && c == 0) flag_index_error(a.err, NVAMD_ERR_POSITION);
+    pos = pos < 0 ? 0 : a.max_positions - 1;
+  }
   float cs[8], sn[8];
   rope_row8(a.cos_sin, pos, c, cs, sn);
   head_norm_rope(lo, hi, w_lo, w_hi, cs, sn, a.eps);
@@ -131,7 +144,7 @@ extern "C" int nvamd_kv_cache_write(const void *k, int64_t k_stride, const void 
   hipLaunchKernelGGL(kv_cache_write_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const u16 *>(k), k_stride, static_cast<const u16 *>(v), v_stride,
                      static_cast<u16 *>(k_cache), static_cast<u16 *>(v_cache), slot_mapping, num_tokens, num_kv_heads,
-                     num_slots);
+                     num_slots, index_error_word());
   return launch_status();
 }
 
@@ -176,6 +189,7 @@ extern "C" int nvamd_qk_norm_rope(void *q, int64_t q_stride, void *k, int64_t k_
   a.num_heads = num_heads;
   a.num_kv_heads = num_kv_heads;
   a.eps = eps;
+  a.err = index_error_word();
   const int vecs = num_heads + num_kv_heads * (store ? 2 : 1);
   const int64_t blocks = ((int64_t)num_tokens * vecs + 31) / 32;
   if (blocks > 0x7fffffff) return NVAMD_EINVAL;

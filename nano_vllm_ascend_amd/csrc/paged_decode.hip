@@ -32,7 +32,7 @@
 // Merge: each wave folds its 8 row groups with DPP and swizzles, wave 0 folds the
 // NW waves through LDS.  A multi-partition unit's wave 0 then publishes
 // (max, sum, acc[128]) per head with agent-scope write-through stores, waits for
-// them, and bumps an arrival counter; the last to arrive reads the partials with
+// them, and bumps a wrapping arrival counter; the last to arrive reads the partials with
 // agent-scope loads, all issued before the first is used, and writes the output.  No L2
 // writeback or invalidate is needed.  Launches with few items (short contexts, small
 // batches) give each (sequence, kv head) one workgroup that covers the whole context
@@ -98,6 +98,7 @@ struct DecodeArgs {
   int max_positions;
   float eps;
   bool store_new;  // this launch stores the new token's k / v (the first of a group's launches)
+  u32 *err;        // index-error word
 };
 
 struct KVTile {
@@ -152,24 +153,35 @@ paged_decode_kernel(DecodeArgs a) {
   const int item = blockIdx.x;
   int b = -1, n_parts = 0, first = 0, ctx = 0;
   int64_t nr = -1;  // fused step: the new token's position (its row in the context)
+  // Index errors seen by this wave (wave-uniform, so it stays in scalar registers); reported with
+  // one atomic after the K/V loop.
+  u32 err_bits = 0;
   if constexpr (WHOLE) {
     // One workgroup per (b, g) covers the whole context bound: the item needs no scan, so the
     // context length, the block-table entries and q are loaded together.
     b = item / hkv;
     n_parts = 1;
     first = b;
-    ctx = max(min(a.context_lens[b], ctx_cap), 0);
+    const int raw = a.context_lens[b];
+    if (raw < 0 || raw > ctx_cap) err_bits |= NVAMD_ERR_CONTEXT;
+    ctx = max(min(raw, ctx_cap), 0);
     if constexpr (FUSED) nr = a.positions[b];
   } else
   for (int b0 = 0, base = 0; b0 < a.batch; b0 += 64) {
     const int bi = b0 + lane;
     int ci = 0, np = 0;
     int64_t pi = 0;
+    bool bad = false;
     if (bi < a.batch) {
-      ci = max(min(a.context_lens[bi], ctx_cap), 0);
+      const int raw = a.context_lens[bi];
+      bad = raw < 0 || raw > ctx_cap;
+      ci = max(min(raw, ctx_cap), 0);
       np = max(ceil_div(ci, PART), 1);
       if constexpr (FUSED) pi = a.positions[bi];  // with the lengths: no later round trip
     }
+    // every sequence is scanned by the workgroup holding its first partition, which reports a
+    // context its table row or the launch's bound cannot hold
+    if (__ballot(bad)) err_bits |= NVAMD_ERR_CONTEXT;
     const int incl = wave_incl_scan(np, lane);
     const int total = __shfl(incl, 63);
     if (item < (base + total) * hkv) {
@@ -274,6 +286,7 @@ paged_decode_kernel(DecodeArgs a) {
     const bool nr_in = nr >= 0 && nr < ctx;
     const bool owner = a.store_new && (nr_in ? (nr >= t_begin && nr < t_end) : (p == n_parts - 1 && w == 0));
     if (t_begin < t_end || owner) {
+      if (owner && (nr < 0 || nr >= a.max_positions)) err_bits |= NVAMD_ERR_POSITION;
       const int64_t pc = nr < 0 ? 0 : (nr >= a.max_positions ? a.max_positions - 1 : nr);
       const float *row = a.cos_sin + pc * D + 8 * c;
       rc0 = *reinterpret_cast<const f32x4 *>(row);
@@ -292,6 +305,7 @@ paged_decode_kernel(DecodeArgs a) {
       rope_row(cs, sn);
       head_norm_rope(k0, k1, ld16(a.k_w + 8 * c), ld16(a.k_w + 64 + 8 * c), cs, sn, a.eps);
       const int64_t slot = a.slots[b];
+      if (slot >= a.num_slots || slot < -1) err_bits |= NVAMD_ERR_SLOT;
       if (r == 0 && slot >= 0 && slot < a.num_slots) {
         const int64_t dst = slot * row_elems + (int64_t)g * D + 8 * c;
         u16 *kc = const_cast<u16 *>(a.k_cache);
@@ -317,7 +331,8 @@ paged_decode_kernel(DecodeArgs a) {
       for (int i = 0; i < TILES; ++i) {
         const int t0 = min(tc + 16 * i, last_tile);
         int blk = (FUSED && CPW == 1) ? first_blk[i] : bt_row[t0 >> a.bs_log2];
-        blk = min(max(blk, 0), a.num_blocks - 1);  // never leave the pool
+        if ((unsigned)blk >= (unsigned)a.num_blocks) err_bits |= NVAMD_ERR_BLOCK;
+        blk = min(max(blk, 0), a.num_blocks - 1);               // never leave the pool
         const int64_t slot = ((int64_t)blk << a.bs_log2) + (t0 & bs_mask) + r;
         const int64_t off = slot * row_elems + (int64_t)g * D + 8 * c;
         const u16 *kp = a.k_cache + off;
@@ -422,6 +437,9 @@ paged_decode_kernel(DecodeArgs a) {
     }
   }
 
+  err_bits = __builtin_amdgcn_readfirstlane(err_bits);
+  if (err_bits != 0 && lane == 0) flag_index_error(a.err, err_bits);
+
   // Wave merge: rescale the 8 row groups to the wave-wide max, then add groups r and r^1
   // (DPP row_ror:8) and r and r^2 (swizzle xor 16).  Lanes 0-31 then hold the sum over
   // groups 0-3 and lanes 32-63 the sum over groups 4-7.
@@ -497,9 +515,13 @@ paged_decode_kernel(DecodeArgs a) {
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // keep the stores above the wait
   __builtin_amdgcn_s_waitcnt(0);
+  // The arrival count wraps: the n_parts-th arrival reads n_parts - 1 and leaves 0 behind, so the
+  // workspace is ready for the next call without a reset store at the end of the merge.
   int *counter = a.counters + (int64_t)b * hkv + g;
   int prev = 0;
-  if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0)
+    prev = (int)__builtin_amdgcn_atomic_inc32(reinterpret_cast<unsigned *>(counter), (unsigned)(n_parts - 1),
+                                              __ATOMIC_RELAXED, "agent");
   prev = __shfl(prev, 0);
   if (prev != n_parts - 1) return;
 
@@ -568,9 +590,6 @@ paged_decode_kernel(DecodeArgs a) {
   for (int j = 0; j < GQA; ++j) {
     const float inv = den[j] > 0.f ? 1.f / den[j] : 0.f;
     *reinterpret_cast<u32 *>(out_base + j * D) = pack_bf16x2(n0[j] * inv, n1[j] * inv);
-  }
-  if (lane == 0) {  // leave the workspace ready for the next call
-    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -686,6 +705,7 @@ int fill_decode_args(DecodeArgs &a, void *out, int64_t out_stride, const void *q
   a.max_ctx = max_context_len;
   a.max_parts = 0;
   a.scale_log2e = scale * kLog2e;
+  a.err = index_error_word();
   return NVAMD_OK;
 }
 

@@ -74,6 +74,7 @@ struct PrefillArgs {
   // a whole group (q_group == GQA, q_head0 == 0) unless the ratio needs several launches.
   int q_group;
   int q_head0;
+  u32 *err;  // index-error word (paged route: contexts past the table row, block ids outside the pool)
 };
 
 // 16 bytes per lane into LDS at lds_base + 16 * lane (LDS-DMA), from a raw buffer (range
@@ -130,7 +131,14 @@ prefill_kernel(PrefillArgs a) {
   const int q_len = a.cu_seqlens_q[s + 1] - q_start;
   if (qt * BQ >= q_len) return;
   int kv_len = PAGED ? a.kv_lens[s] : q_len;
-  if (PAGED) kv_len = min(kv_len, a.bt_width << a.bs_log2);
+  if (PAGED) {
+    const int cap = a.bt_width << a.bs_log2;
+    // a context its table row cannot hold (or shorter than its queries): report once per sequence;
+    // the table is read only up to its width
+    if ((kv_len > cap || kv_len < q_len) && g == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+      flag_index_error(a.err, NVAMD_ERR_CONTEXT);
+    kv_len = min(kv_len, cap);
+  }
   const int offset = kv_len - q_len;  // query row r sees keys 0..offset+r
 
   const int tid = threadIdx.x;
@@ -221,8 +229,11 @@ prefill_kernel(PrefillArgs a) {
       const int k0 = min(t * kBK, kv_len - 1), k1 = min(t * kBK + 16, kv_len - 1);
       typedef const __attribute__((address_space(4))) int32_t const_i32;
       const_i32 *btc = (const_i32 *)bt_row;
-      const int b0 = min(max(btc[k0 >> a.bs_log2], 0), a.num_blocks - 1);
-      const int b1 = min(max(btc[k1 >> a.bs_log2], 0), a.num_blocks - 1);
+      const int e0 = btc[k0 >> a.bs_log2], e1 = btc[k1 >> a.bs_log2];
+      if (((unsigned)e0 >= (unsigned)a.num_blocks || (unsigned)e1 >= (unsigned)a.num_blocks) && tid == 0)
+        flag_index_error(a.err, NVAMD_ERR_BLOCK);  // never leave the pool; report the entry
+      const int b0 = min(max(e0, 0), a.num_blocks - 1);
+      const int b1 = min(max(e1, 0), a.num_blocks - 1);
       const u32 block_bytes = (u32)((cache_row << a.bs_log2) * 2);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -448,6 +459,7 @@ extern "C" int nvamd_varlen_prefill(void *out, int64_t out_stride, const void *q
   a.cu_seqlens_q = cu_seqlens_q;
   a.num_kv_heads = num_kv_heads;
   a.scale_log2e = scale * kLog2e;
+  a.err = index_error_word();
   return dispatch<false>(a, n_seqs, num_heads / num_kv_heads, max_q_len, stream);
 }
 
@@ -482,5 +494,6 @@ extern "C" int nvamd_paged_prefill(void *out, int64_t out_stride, const void *q,
   a.kv_lens = kv_lens;
   a.num_kv_heads = num_kv_heads;
   a.scale_log2e = scale * kLog2e;
+  a.err = index_error_word();
   return dispatch<true>(a, n_seqs, num_heads / num_kv_heads, max_q_len, stream);
 }

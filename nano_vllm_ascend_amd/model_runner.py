@@ -49,19 +49,23 @@ DEFAULT_DECODE_GRAPH_BATCH_SIZES = [1, 2, 4, 8, 16, 32]
 
 
 class _TokenFetch:
-    """A pinned host copy of one step's greedy ids and the event that says it has landed."""
+    """A pinned host copy of one step's greedy ids and of the device's index-error word, and the
+    event that says both have landed."""
 
-    def __init__(self, n: int):
+    def __init__(self, n: int, errors):
         self.buf = torch.empty(n, dtype=torch.int64, pin_memory=True)
+        self.errors = errors
         self.event = torch.cuda.Event()
 
     def start(self, ids: torch.Tensor) -> "_TokenFetch":
         self.buf.copy_(ids, non_blocking=True)
+        self.errors.fetch()
         self.event.record()
         return self
 
     def tokens(self) -> list[int]:
         self.event.synchronize()
+        self.errors.raise_if_set()  # an index the reference would have refused: IndexError
         return self.buf.tolist()
 
 
@@ -145,6 +149,10 @@ class ModelRunner:
         self._prefilled_since_decode = False
         self._fetch: dict[int, list] = {}      # batch size -> [two _TokenFetch, next index]
         self._logits_keep: dict[int, torch.Tensor] = {}
+        # the device's index-error word, read with every step's tokens (a factory so a test can
+        # stand in for the device)
+        self.error_word_factory = _C.IndexErrorWord
+        self._eager_errors = None
         self.overlap_stats = {"launched": 0, "used": 0, "discarded": 0}
         # prefill batches, those on the paged (prefix-hit) route, and the prompt tokens whose K/V
         # came from the prefix cache instead of being computed
@@ -223,10 +231,17 @@ class ModelRunner:
 
     # ------------------------------------------------------------ sampling
     def _sample(self, logits: torch.Tensor, seqs: list[Sequence], greedy_ids: torch.Tensor | None = None) -> list[int]:
+        if self._eager_errors is None:
+            self._eager_errors = self.error_word_factory()
+        self._eager_errors.fetch()  # queued behind the step's kernels, read with its tokens
         if all(seq.sampling_params.is_greedy() for seq in seqs):
             ids = greedy_ids if greedy_ids is not None else _C.argmax_rows(logits)
-            return ids.tolist()  # one device-to-host read for the batch
-        return [int(self.sampler.sample(logits[i : i + 1], seq.sampling_params).item()) for i, seq in enumerate(seqs)]
+            tokens = ids.tolist()  # one device-to-host read for the batch
+        else:
+            tokens = [int(self.sampler.sample(logits[i : i + 1], seq.sampling_params).item())
+                      for i, seq in enumerate(seqs)]
+        self._eager_errors.raise_if_set()
+        return tokens
 
     # ------------------------------------------------------------- forward
     def _drop_in_flight(self) -> None:
@@ -280,7 +295,8 @@ class ModelRunner:
     def _fetch_tokens(self, b: int, ids: torch.Tensor) -> _TokenFetch:
         slot = self._fetch.get(b)
         if slot is None:
-            slot = self._fetch[b] = [_TokenFetch(b), _TokenFetch(b), 0]
+            slot = self._fetch[b] = [_TokenFetch(b, self.error_word_factory()),
+                                     _TokenFetch(b, self.error_word_factory()), 0]
         f = slot[slot[2]]
         slot[2] ^= 1  # ping-pong: the step launched ahead uses the other buffer
         return f.start(ids)

@@ -207,12 +207,30 @@ class LiveGraphRunner(DecodeGraphRunner):
         return entry.logits
 
 
+class HostErrorWord:
+    """Stands in for the device's index-error word: a host flag that a test can raise."""
+
+    pending = 0  # bits the next fetch will find
+
+    def __init__(self):
+        self.bits = 0
+
+    def fetch(self):
+        self.bits, HostErrorWord.pending = HostErrorWord.pending, 0
+
+    def raise_if_set(self):
+        if self.bits:
+            bits, self.bits = self.bits, 0
+            raise IndexError(f"index out of range in the step's kernels: {_C.describe_index_errors(bits)}")
+
+
 def make_llm(monkeypatch, *, block_size, num_blocks, max_num_seqs, prefix, overlap, max_model_len=1024,
              sizes=(1, 2, 4, 8)) -> LLM:
     monkeypatch.setattr(_C, "argmax_rows", lambda logits, out=None: logits.argmax(-1))
     monkeypatch.setattr(_C, "alloc_paged_decode_workspace", lambda *a, **k: None)
     runner = object.__new__(ModelRunner)
     runner._init_step_state(overlap)
+    runner.error_word_factory = HostErrorWord
     runner.device = torch.device("cpu")
     runner.block_size, runner.max_model_len = block_size, max_model_len
     runner.enable_prefix_cache, runner.enable_decode_graph = prefix, True
@@ -339,3 +357,30 @@ def test_continuation_after_eos_does_not_take_a_stale_step(monkeypatch):
         results[overlap] = (a, b, dict(llm.runner.overlap_stats))
     assert results[True][:2] == results[False][:2]
     assert results[True][2]["discarded"] > 0 and results[True][2]["launched"] > 0
+
+
+def test_index_error_reported_by_the_kernels_raises_after_the_step(monkeypatch):
+    """Where the reference's indexing raises, the kernels set a bit in the device's error word; the
+    runner reads the word with the step's tokens and raises IndexError from that step, before its
+    tokens are applied (eager sampling path: prefill and uncaptured decode)."""
+    cfg = dict(block_size=16, num_blocks=40, max_num_seqs=2, prefix=False)
+    llm = make_llm(monkeypatch, overlap=False, sizes=(), **cfg)
+    ids = [llm.submit(list(range(20)), max_new_tokens=6), llm.submit(list(range(5, 40)), max_new_tokens=6)]
+    llm.step()  # prefill: clean
+    llm.step()  # decode: clean
+    seqs = [llm.scheduler.seqs[i] for i in ids]
+    # a decode step first commits each sequence's pending token, then runs the forward that samples
+    # the next one
+    committed = [list(s.generated_token_ids) + [s.next_token_id] for s in seqs]
+    HostErrorWord.pending = _C.ERR_SLOT  # the next step's kernels skip an out-of-range slot
+    with pytest.raises(IndexError, match="slot_mapping entry outside the KV cache"):
+        llm.step()
+    # the failed forward's tokens were not taken
+    assert [list(s.generated_token_ids) for s in seqs] == committed
+    assert all(s.next_token_id is None or s.next_token_id == c[-1] for s, c in zip(seqs, committed))
+
+
+def test_index_error_bits_are_described():
+    assert "RoPE table" in _C.describe_index_errors(_C.ERR_POSITION)
+    text = _C.describe_index_errors(_C.ERR_CONTEXT | _C.ERR_BLOCK | 64)
+    assert "block-table row" in text and "block pool" in text and "unknown bits 0x40" in text
