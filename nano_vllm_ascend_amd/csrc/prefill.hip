@@ -311,7 +311,13 @@ prefill_kernel(PrefillArgs a) {
     const int base = t * kBK;
     if (visible(t)) {
       f32x16 sc;
+      // Wave priority: the score MFMAs issue at priority 0 and the rest of the tile (mask,
+      // softmax, P V) at 1, so a wave in its softmax is not held back by another wave's score
+      // MFMAs on the same SIMD (the two do not overlap on gfx950).  1.4% faster on 32 x U[64,
+      // 2048] than one priority throughout; raising the softmax alone measured 1.5% slower.
+      __builtin_amdgcn_s_setprio(0);
       score(sk, sc);
+      __builtin_amdgcn_s_setprio(1);
       // mask; key of register i: base + 8(i/4) + 4hl + i%4.  The running max is taken on raw
       // scores (scale > 0) and applied in the exponent's FMA.  Only tiles that cross this
       // wave's diagonal or the end of the keys need the mask (1-2 per wave); the test is
