@@ -195,8 +195,11 @@ skinny_gemm_kernel(GemmArgs a) {
   const int k_begin = slice * a.k_slice;
   const int k_end = k_begin + a.k_slice;
   const int k_first = k_begin + w * WK;
-#pragma unroll 1
-  for (int k0 = k_first; k0 < k_end; k0 += RK) {
+  // One K round: issue every load of the round before the first MFMA waits on one; in the first
+  // round (NORM) finish rstd from the sums of squares, whose loads were issued before the round's.
+  // The first round is written out ahead of the loop: inside the loop the compiler hoisted the
+  // sums above the first round's loads, so the weight stream waited for the sums' round trip.
+  auto k_round = [&](const int k0, const bool first) {
     u32x4 wv[KB][NACC], xv[KB][MT], nv[NORM ? KB : 1];
 #pragma unroll
     for (int b = 0; b < KB; ++b) {
@@ -206,9 +209,8 @@ skinny_gemm_kernel(GemmArgs a) {
       for (int mt = 0; mt < MT; ++mt) xv[b][mt] = ld16(xp[mt] + (int64_t)(k0 + 32 * b) * xs);
       if (NORM) nv[b] = ld16(np + k0 + 32 * b);
     }
-    // every load of the round is issued before the first MFMA waits on one
     __builtin_amdgcn_sched_barrier(0);
-    if (NORM && k0 == k_first) {
+    if (NORM && first) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         float ss = 0.f;
@@ -234,6 +236,11 @@ skinny_gemm_kernel(GemmArgs a) {
       }
       mfma_step<NACC, MT>(acc, xa, wv[b]);
     }
+  };
+  if (k_first < k_end) {
+    k_round(k_first, true);
+#pragma unroll 1
+    for (int k0 = k_first + RK; k0 < k_end; k0 += RK) k_round(k0, false);
   }
 
   // C register i of lane (n, g) in M tile mt is row 16*mt + 4*g + i, column n of the tile.
