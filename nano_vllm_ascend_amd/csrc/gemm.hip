@@ -77,12 +77,19 @@ __device__ __forceinline__ void store_agent4(float *p, f32x4 v) {
   __hip_atomic_store(reinterpret_cast<uint64_t *>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(reinterpret_cast<uint64_t *>(p) + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ f32x4 load_agent4(const float *p) {
-  uint64_t *q = reinterpret_cast<uint64_t *>(const_cast<float *>(p));
-  const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return f32x4{__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
-               __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32))};
+
+// Sum over the NW waves' partial tiles of element e (4 floats) of tile t, added in wave order;
+// every LDS read is issued before the first add (the compiler otherwise waits after each read).
+template <int NW, int NACC>
+__device__ __forceinline__ f32x4 sum_waves(const float (&s_c)[NW][NACC][32 * 16], int t, int e) {
+  f32x4 r[NW];
+#pragma unroll
+  for (int x = 0; x < NW; ++x) r[x] = *reinterpret_cast<const f32x4 *>(&s_c[x][t][e]);
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 s = r[0];
+#pragma unroll
+  for (int x = 1; x < NW; ++x) s += r[x];
+  return s;
 }
 
 // One 32-wide K step of a wave: W tiles wv[t], X M-tiles xv[mt] (already normalised).
@@ -259,10 +266,7 @@ skinny_gemm_kernel(GemmArgs a) {
     for (int u = tid; u < NACC * TF / 4; u += kNW * 64) {
       const int t = u / (TF / 4);
       const int e = 4 * (u % (TF / 4));
-      f32x4 s = *reinterpret_cast<const f32x4 *>(&s_c[0][t][e]);
-#pragma unroll
-      for (int x = 1; x < kNW; ++x) s += *reinterpret_cast<const f32x4 *>(&s_c[x][t][e]);
-      store_agent4(part + ((int64_t)slice * NACC + t) * TF + e, s);
+      store_agent4(part + ((int64_t)slice * NACC + t) * TF + e, sum_waves<kNW, NACC>(s_c, t, e));
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keep the stores above the wait
     __builtin_amdgcn_s_waitcnt(0);
@@ -288,20 +292,24 @@ skinny_gemm_kernel(GemmArgs a) {
     for (int h = 0; h < NV; ++h) {
       const int tt = t + h * NT;
       if (a.ks > 1) {
+        // The ks published slices through one agent-coherent buffer range: eight slices' loads in
+        // flight per step, and loads past the last slice return zeros without a memory access.
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            part, 0, a.ks * NACC * TF * (int)sizeof(float), kBufferRsrcWord3);
         v[h] = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < a.ks; s0 += 8) {  // eight slices' loads in flight per step
+        for (int s0 = 0; s0 < a.ks; s0 += 8) {
           f32x4 ld[8];
 #pragma unroll
           for (int q = 0; q < 8; ++q)
-            ld[q] = load_agent4(part + ((int64_t)min(s0 + q, a.ks - 1) * NACC + tt) * TF + e);
+            ld[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rsrc, (((s0 + q) * NACC + tt) * TF + e) * (int)sizeof(float), 0,
+                                                  kCachePolicyAgent));
 #pragma unroll
           for (int q = 0; q < 8; ++q)
             if (s0 + q < a.ks) v[h] += ld[q];
         }
       } else {
-        v[h] = *reinterpret_cast<const f32x4 *>(&s_c[0][tt][e]);
-#pragma unroll
-        for (int x = 1; x < kNW; ++x) v[h] += *reinterpret_cast<const f32x4 *>(&s_c[x][tt][e]);
+        v[h] = sum_waves<kNW, NACC>(s_c, tt, e);
       }
     }
     const int c = n0 + cl;
