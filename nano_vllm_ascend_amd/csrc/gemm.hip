@@ -71,12 +71,6 @@ struct GemmArgs {
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
 
-__device__ __forceinline__ void store_agent4(float *p, f32x4 v) {
-  const uint64_t lo = (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32);
-  const uint64_t hi = (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(reinterpret_cast<uint64_t *>(p) + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Sum over the NW waves' partial tiles of element e (4 floats) of tile t, added in wave order;
 // every LDS read is issued before the first add (the compiler otherwise waits after each read).
@@ -263,10 +257,14 @@ skinny_gemm_kernel(GemmArgs a) {
 
   float *part = a.partials + ((int64_t)group * a.ks) * NACC * TF;
   if (a.ks > 1) {
+    // this slice's partial tiles, written through to memory with 16-byte agent-coherent stores
+    const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(
+        part, 0, a.ks * NACC * TF * (int)sizeof(float), kBufferRsrcWord3);
     for (int u = tid; u < NACC * TF / 4; u += kNW * 64) {
       const int t = u / (TF / 4);
       const int e = 4 * (u % (TF / 4));
-      store_agent4(part + ((int64_t)slice * NACC + t) * TF + e, sum_waves<kNW, NACC>(s_c, t, e));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum_waves<kNW, NACC>(s_c, t, e)), prsrc,
+                                             ((slice * NACC + t) * TF + e) * (int)sizeof(float), 0, kCachePolicyAgent);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keep the stores above the wait
     __builtin_amdgcn_s_waitcnt(0);
