@@ -117,17 +117,37 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
-// Two adjacent floats (8-byte aligned) as one agent-scope 64-bit access.
-__device__ __forceinline__ void store_agent2(float *p, float lo, float hi) {
-  const uint64_t v = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// 2 * GQA consecutive floats of a partial record through an agent-coherent buffer range
+// (write-through stores, loads that bypass the non-coherent caches): 8 bytes for one head,
+// 16-byte pieces for two or four.
+template <int GQA>
+__device__ __forceinline__ void store_block(__amdgpu_buffer_rsrc_t rsrc, int byte_off, const float (&v)[2 * GQA]) {
+  if constexpr (GQA == 1) {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(v[0]), __float_as_uint(v[1])}, rsrc, byte_off, 0,
+                                          kCachePolicyAgent);
+  } else {
+#pragma unroll
+    for (int h = 0; h < GQA / 2; ++h)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(v[4 * h]), __float_as_uint(v[4 * h + 1]), __float_as_uint(v[4 * h + 2]),
+                __float_as_uint(v[4 * h + 3])},
+          rsrc, byte_off + 16 * h, 0, kCachePolicyAgent);
+  }
 }
-
-__device__ __forceinline__ void load_agent2(const float *p, float &lo, float &hi) {
-  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(p)), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-  lo = __uint_as_float((uint32_t)v);
-  hi = __uint_as_float((uint32_t)(v >> 32));
+template <int GQA>
+__device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t rsrc, int byte_off, float (&v)[2 * GQA]) {
+  if constexpr (GQA == 1) {
+    const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rsrc, byte_off, 0, kCachePolicyAgent);
+    v[0] = __uint_as_float(x[0]);
+    v[1] = __uint_as_float(x[1]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < GQA / 2; ++h) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_off + 16 * h, 0, kCachePolicyAgent);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * h + e] = __uint_as_float(x[e]);
+    }
+  }
 }
 
 // GQA 1, and GQA 2 with one chunk per wave, fit 128 VGPRs without spills: four waves
@@ -504,14 +524,30 @@ paged_decode_kernel(DecodeArgs a) {
     return;
   }
 
-  // Publish (max, sum, acc[128]) per head with write-through stores, wait for them, then
-  // count the arrival.  The last wave 0 of (b, g) to arrive merges all partitions.
-  float *part_base = a.partials + (((int64_t)b * hkv + g) * a.max_parts) * GQA * kPartFloats;
+  // A partition's record (GQA * kPartFloats floats): the heads' (max, sum) pairs, then lane l's
+  // accumulators of every head (dims 2l, 2l+1 of head j at 2j, 2j+1), 2 * GQA floats at
+  // kHdr + 2 * GQA * l, so a lane publishes and reads its share of a partition in 16-byte pieces.
+  constexpr int kRec = GQA * kPartFloats;
+  constexpr int kHdr = GQA <= 2 ? 4 : 2 * GQA;
+  static_assert(kHdr + 2 * GQA * 64 <= kRec, "partial record");
+  float *part_base = a.partials + (((int64_t)b * hkv + g) * a.max_parts) * kRec;
+  // Buffer range over exactly the n_parts partitions: reads past them return zeros without a
+  // memory access.
+  const __amdgpu_buffer_rsrc_t parts_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(part_base, 0, n_parts * kRec * (int)sizeof(float), kBufferRsrcWord3);
+  // Publish with write-through stores, wait for them, then count the arrival.  The last wave 0
+  // of (b, g) to arrive merges all partitions.
+  {
+    float blk[2 * GQA], hdr[2 * GQA];
 #pragma unroll
-  for (int j = 0; j < GQA; ++j) {
-    float *pr = part_base + ((int64_t)p * GQA + j) * kPartFloats;
-    store_agent2(pr + 2 + 2 * lane, acc[j][0], acc[j][1]);
-    if (lane == 0) store_agent2(pr, mx[j], ls[j]);
+    for (int j = 0; j < GQA; ++j) {
+      blk[2 * j] = acc[j][0];
+      blk[2 * j + 1] = acc[j][1];
+      hdr[2 * j] = mx[j];
+      hdr[2 * j + 1] = ls[j];
+    }
+    store_block<GQA>(parts_rsrc, (p * kRec + kHdr + 2 * GQA * lane) * (int)sizeof(float), blk);
+    if (lane == 0) store_block<GQA>(parts_rsrc, p * kRec * (int)sizeof(float), hdr);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // keep the stores above the wait
   __builtin_amdgcn_s_waitcnt(0);
@@ -528,27 +564,25 @@ paged_decode_kernel(DecodeArgs a) {
   // Merge.  Lane x holds partition x's (max, sum) of every head; the accumulators of the
   // first MP partitions are loaded in the same round (every load issued before the first
   // use, so the merge waits for one memory round trip), later ones 8 partitions per round.
-  // The first round uses buffer loads over exactly the n_parts published partitions: the
-  // range check returns zeros past them without a branch or a memory access.
   constexpr int MP = GQA <= 2 ? 16 : 8;
-  const __amdgpu_buffer_rsrc_t parts_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      part_base, 0, n_parts * GQA * kPartFloats * (int)sizeof(float), kBufferRsrcWord3);
   float pm[GQA], pl[GQA], v0f[GQA][MP], v1f[GQA][MP];
+  {
+    float hx[2 * GQA];
+    load_block<GQA>(parts_rsrc, lane * kRec * (int)sizeof(float), hx);
 #pragma unroll
-  for (int j = 0; j < GQA; ++j) {
-    const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(
-        parts_rsrc, (lane * GQA + j) * kPartFloats * (int)sizeof(float), 0, kCachePolicyAgent);
-    pm[j] = lane < n_parts ? __uint_as_float(ml[0]) : -INFINITY;
-    pl[j] = __uint_as_float(ml[1]);
+    for (int j = 0; j < GQA; ++j) {
+      pm[j] = lane < n_parts ? hx[2 * j] : -INFINITY;
+      pl[j] = hx[2 * j + 1];
+    }
   }
 #pragma unroll
   for (int k = 0; k < MP; ++k) {
+    float vk[2 * GQA];
+    load_block<GQA>(parts_rsrc, (k * kRec + kHdr + 2 * GQA * lane) * (int)sizeof(float), vk);
 #pragma unroll
     for (int j = 0; j < GQA; ++j) {
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
-          parts_rsrc, ((k * GQA + j) * kPartFloats + 2 + 2 * lane) * (int)sizeof(float), 0, kCachePolicyAgent);
-      v0f[j][k] = __uint_as_float(v[0]);
-      v1f[j][k] = __uint_as_float(v[1]);
+      v0f[j][k] = vk[2 * j];
+      v1f[j][k] = vk[2 * j + 1];
     }
   }
   float fx[GQA], den[GQA], n0[GQA], n1[GQA];
@@ -569,10 +603,13 @@ paged_decode_kernel(DecodeArgs a) {
     float v0[GQA][8], v1[GQA][8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int x = min(x0 + k, n_parts - 1);
+      float vk[2 * GQA];
+      load_block<GQA>(parts_rsrc, ((x0 + k) * kRec + kHdr + 2 * GQA * lane) * (int)sizeof(float), vk);
 #pragma unroll
-      for (int j = 0; j < GQA; ++j)
-        load_agent2(part_base + ((int64_t)x * GQA + j) * kPartFloats + 2 + 2 * lane, v0[j][k], v1[j][k]);
+      for (int j = 0; j < GQA; ++j) {
+        v0[j][k] = vk[2 * j];
+        v1[j][k] = vk[2 * j + 1];
+      }
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
