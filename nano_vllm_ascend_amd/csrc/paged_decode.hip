@@ -107,14 +107,18 @@ struct KVTile {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave, in registers: a Hillis-Steele scan inside
+// each 16-lane row by DPP row shifts (lanes shifted in from outside the row read 0), then each
+// row adds the totals of the rows before it (lane 15 of each row, read into scalar registers).
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t = __shfl_up(v, d);
-    if (lane >= d) v += t;
-  }
-  return v;
+  v += __builtin_amdgcn_mov_dpp(v, 0x111, 0xF, 0xF, true);  // row_shr:1
+  v += __builtin_amdgcn_mov_dpp(v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += __builtin_amdgcn_mov_dpp(v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += __builtin_amdgcn_mov_dpp(v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+  const int r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane >> 4;
+  return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
 // 2 * GQA consecutive floats of a partial record through an agent-coherent buffer range
@@ -203,16 +207,18 @@ paged_decode_kernel(DecodeArgs a) {
     // context its table row or the launch's bound cannot hold
     if (__ballot(bad)) err_bits |= NVAMD_ERR_CONTEXT;
     const int incl = wave_incl_scan(np, lane);
-    const int total = __shfl(incl, 63);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
     if (item < (base + total) * hkv) {
       const uint64_t past = __ballot((base + incl) * hkv > item);
       const int sel = __ffsll((unsigned long long)past) - 1;
       b = b0 + sel;
-      n_parts = __shfl(np, sel);
-      first = base + __shfl(incl, sel) - n_parts;
-      ctx = __shfl(ci, sel);
+      // sel is wave-uniform (a ballot): read the chosen lane's values into scalar registers
+      n_parts = __builtin_amdgcn_readlane(np, sel);
+      first = base + __builtin_amdgcn_readlane(incl, sel) - n_parts;
+      ctx = __builtin_amdgcn_readlane(ci, sel);
       if constexpr (FUSED) {
-        const int lo = __shfl((int)(uint32_t)pi, sel), hi = __shfl((int)(pi >> 32), sel);
+        const int lo = __builtin_amdgcn_readlane((int)(uint32_t)pi, sel);
+        const int hi = __builtin_amdgcn_readlane((int)(pi >> 32), sel);
         nr = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
       }
       break;
