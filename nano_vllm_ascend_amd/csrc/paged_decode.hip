@@ -353,10 +353,15 @@ paged_decode_kernel(DecodeArgs a) {
 #pragma unroll 1
     for (int tc = t_begin; tc < t_end; tc += CT) {
       KVTile T[TILES];
+      // the chunk's block-table entries first, so their scalar loads share one wait
+      int blk_t[TILES];
+#pragma unroll
+      for (int i = 0; i < TILES; ++i)
+        blk_t[i] = (FUSED && CPW == 1) ? first_blk[i] : bt_row[min(tc + 16 * i, last_tile) >> a.bs_log2];
 #pragma unroll
       for (int i = 0; i < TILES; ++i) {
         const int t0 = min(tc + 16 * i, last_tile);
-        int blk = (FUSED && CPW == 1) ? first_blk[i] : bt_row[t0 >> a.bs_log2];
+        int blk = blk_t[i];
         if ((unsigned)blk >= (unsigned)a.num_blocks) err_bits |= NVAMD_ERR_BLOCK;
         blk = min(max(blk, 0), a.num_blocks - 1);               // never leave the pool
         const int64_t slot = ((int64_t)blk << a.bs_log2) + (t0 & bs_mask) + r;
