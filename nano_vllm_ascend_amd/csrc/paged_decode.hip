@@ -325,12 +325,15 @@ paged_decode_kernel(DecodeArgs a) {
     if (owner) {
       const u16 *kp = a.k_new + (int64_t)b * a.k_new_stride + g * D + 8 * c;
       const u16 *vp = a.v_new + (int64_t)b * a.v_new_stride + g * D + 8 * c;
+      // every load of the store issued together, before any of it is used
       u32x4 k0 = ld16(kp), k1 = ld16(kp + 64);
       const u32x4 v0 = ld16(vp), v1 = ld16(vp + 64);
+      const u32x4 kw0 = ld16(a.k_w + 8 * c), kw1 = ld16(a.k_w + 64 + 8 * c);
+      const int64_t slot = a.slots[b];
+      __builtin_amdgcn_sched_barrier(0);
       float cs[8], sn[8];
       rope_row(cs, sn);
-      head_norm_rope(k0, k1, ld16(a.k_w + 8 * c), ld16(a.k_w + 64 + 8 * c), cs, sn, a.eps);
-      const int64_t slot = a.slots[b];
+      head_norm_rope(k0, k1, kw0, kw1, cs, sn, a.eps);
       if (slot >= a.num_slots || slot < -1) err_bits |= NVAMD_ERR_SLOT;
       if (r == 0 && slot >= 0 && slot < a.num_slots) {
         const int64_t dst = slot * row_elems + (int64_t)g * D + 8 * c;
