@@ -18,10 +18,12 @@
 //     a tiled X holds 16 * ceil(M/16) rows, and rows past M only reach dropped outputs;
 //   * a workgroup of NW waves owns 16*NT output columns, one of KS slices of K
 //     (split-K across workgroups where the column count alone gives too few
-//     workgroups) and one 32-row slab of X (M > 32: ceil(M/32) slabs, the slab index
-//     fastest in the grid, so the slabs reading one weight tile run side by side and
-//     its repeat reads come from the Infinity Cache); its waves split the slice again,
-//     and a wave's NT column tiles share each A fragment;
+//     workgroups) and one slab of X: up to 32 rows, or above 32 rows 64-row slabs of four M
+//     tiles (32-row slabs where a NORM prologue's k exceeds 1024 or it feeds a residual
+//     epilogue), the slab index fastest in the grid, so the slabs reading one weight tile
+//     run side by side and its repeat reads come from the Infinity Cache; its waves split
+//     the slice again, and a wave's NT column tiles share each A fragment (64-row slabs of
+//     the vocabulary-sized projection: 64 columns per workgroup instead of 128);
 //   * the waves' partial tiles meet in LDS; with KS > 1 the workgroups publish fp32
 //     partials with agent-scope write-through stores, count arrivals per column group,
 //     and the last to arrive adds the KS partials in slice order.  Every sum has a
@@ -46,6 +48,9 @@ constexpr int kCounterSlots = 4096;    // arrival counters at the front of the w
 constexpr size_t kCounterBytes = kCounterSlots * sizeof(int);
 constexpr int kMaxNormK = 2048;  // NORM prologue: k <= 2048
 constexpr int kSsqVec = kMaxNormK / 128 / 4;  // 16-byte partial-sum loads per lane
+// 64-row slabs (MT = 4 M tiles): the NORM prologue then takes k <= 1024, so a lane's partial sums
+// fit two 16-byte loads per M tile.
+constexpr int kMaxWideNormK = 1024;
 
 struct GemmArgs {
   const u16 *x;
@@ -74,8 +79,8 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)
 
 // Sum over the NW waves' partial tiles of element e (4 floats) of tile t, added in wave order;
 // every LDS read is issued before the first add (the compiler otherwise waits after each read).
-template <int NW, int NACC>
-__device__ __forceinline__ f32x4 sum_waves(const float (&s_c)[NW][NACC][32 * 16], int t, int e) {
+template <int NW, int NACC, int TF>
+__device__ __forceinline__ f32x4 sum_waves(const float (&s_c)[NW][NACC][TF], int t, int e) {
   f32x4 r[NW];
 #pragma unroll
   for (int x = 0; x < NW; ++x) r[x] = *reinterpret_cast<const f32x4 *>(&s_c[x][t][e]);
@@ -105,7 +110,10 @@ skinny_gemm_kernel(GemmArgs a) {
   constexpr int CW = 16 * NT;                           // output columns of the workgroup
   constexpr int WK = 32 * KB;                           // K per wave per round
   constexpr int RK = kNW * WK;                          // K per workgroup per round
-  constexpr int TF = 32 * 16;                           // floats of one 32-row x 16-column tile
+  constexpr int SR = MT <= 2 ? 32 : 16 * MT;            // rows of the workgroup's slab
+  constexpr int TF = SR * 16;                           // floats of one slab-row x 16-column tile
+  constexpr int kSsqV = MT <= 2 ? kSsqVec : kMaxWideNormK / 128 / 4;
+  static_assert(MT == 1 || MT == 2 || MT == 4, "32-row slabs of one or two M tiles, or 64-row slabs");
   static_assert(EPI != kEpiResid || CW % 32 == 0,
                 "the residual epilogue's sums of squares need whole 32-column groups in one workgroup");
   const int tid = threadIdx.x;
@@ -113,27 +121,27 @@ skinny_gemm_kernel(GemmArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  // Grid: (column group, K slice[, 32-row slab]), slab fastest (SLABS: M > 32).  A slab's rows
-  // become rows 0..31 of this workgroup: operand, norm-partial and output pointers move to its
+  // Grid: (column group, K slice[, slab of SR rows]), slab fastest (SLABS: M > SR).  A slab's rows
+  // become rows 0..SR-1 of this workgroup: operand, norm-partial and output pointers move to its
   // first row, and its split-K partials and counters follow those of the earlier slabs.
-  const int slabs = SLABS ? (a.m + 31) >> 5 : 1;
+  const int slabs = SLABS ? (a.m + SR - 1) / SR : 1;
   const int slab = SLABS ? blockIdx.x % slabs : 0;
   const int gs = SLABS ? blockIdx.x / slabs : blockIdx.x;
   const int group = gs / a.ks;
   const int slice = gs - group * a.ks;
   const int n0 = group * CW;
   if (SLABS && slab > 0) {
-    const int64_t r0 = 32 * (int64_t)slab;
-    a.x += a.x_tiled ? 2 * slab * (int64_t)(a.k >> 5) * 512 : r0 * a.x_stride;
+    const int64_t r0 = SR * (int64_t)slab;
+    a.x += a.x_tiled ? MT * slab * (int64_t)(a.k >> 5) * 512 : r0 * a.x_stride;
     if (NORM) a.x_ssq += r0 * (a.k >> 5);
-    a.y += a.y_tiled ? 2 * slab * (int64_t)(a.n >> 5) * 512 : r0 * a.y_stride;
+    a.y += a.y_tiled ? MT * slab * (int64_t)(a.n >> 5) * 512 : r0 * a.y_stride;
     if (EPI == kEpiResid) a.y_ssq += r0 * (a.n >> 5);
     const int groups = gridDim.x / (slabs * a.ks);
     a.counters += slab * groups;
     a.partials += (int64_t)slab * groups * a.ks * NACC * TF;
-    a.m -= 32 * slab;
+    a.m -= SR * slab;
   }
-  if (SLABS) a.m = min(a.m, 32);
+  if (SLABS) a.m = min(a.m, SR);
 
   // Operand addresses: base + k0 * step for the 32-wide K step starting at k0 (tiled: the
   // step's 512-element tile follows the previous one, so 16 elements per unit of k).
@@ -145,7 +153,7 @@ skinny_gemm_kernel(GemmArgs a) {
     xr[mt] = min(16 * mt + n, a.m - 1);
     // a tiled X holds 16 * ceil(M/16) rows: an M tile past the slab's last row re-reads its last
     // tile (those rows only reach dropped outputs)
-    const int mt_x = SLABS ? min(mt, (a.m - 1) >> 4) : mt;
+    const int mt_x = SLABS || MT > 2 ? min(mt, (a.m - 1) >> 4) : mt;
     xp[mt] = a.x_tiled ? a.x + (int64_t)mt_x * (a.k >> 5) * 512 + 8 * lane : a.x + (int64_t)xr[mt] * a.x_stride + 8 * g;
   }
   const u16 *wp[NACC];
@@ -160,7 +168,7 @@ skinny_gemm_kernel(GemmArgs a) {
   // of squares (k <= 2048: at most four 16-byte loads).  They are issued before the weight
   // loads, so rstd is ready while the weights are in flight.
   float rstd[MT];
-  f32x4 sv[MT][kSsqVec];
+  f32x4 sv[MT][kSsqV];
   const int ssq_q = a.k >> 7;  // partials per lane
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -168,7 +176,7 @@ skinny_gemm_kernel(GemmArgs a) {
     if (NORM) {
       const float *sp = a.x_ssq + (int64_t)xr[mt] * (a.k >> 5) + g * ssq_q;
 #pragma unroll
-      for (int i = 0; i < kSsqVec; ++i)
+      for (int i = 0; i < kSsqV; ++i)
         sv[mt][i] = 4 * i < ssq_q ? *reinterpret_cast<const f32x4 *>(sp + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
@@ -177,13 +185,18 @@ skinny_gemm_kernel(GemmArgs a) {
   // read now so that their load overlaps the weight stream instead of following the merge.  Only
   // this column group's merging workgroup writes them, after every read of this launch.
   constexpr int kRowUnits = CW / 4;
-  static_assert(EPI != kEpiResid || 32 * kRowUnits <= kNW * 64, "RESID: one epilogue unit per thread");
-  u32x2 resid = {0u, 0u};
+  constexpr int kUnits = SR * kRowUnits;                      // epilogue units of the workgroup
+  constexpr int kUPT = (kUnits + kNW * 64 - 1) / (kNW * 64);  // units per thread: u = tid + j * threads
+  u32x2 resid[kUPT] = {};
   if constexpr (EPI == kEpiResid) {
-    if (tid < 32 * kRowUnits) {
-      const int rr = min(tid / kRowUnits, a.m - 1);
-      const int c = n0 + 4 * (tid % kRowUnits);
-      resid = *reinterpret_cast<const u32x2 *>(a.y + (a.y_tiled ? tiled_index(rr, c, a.n) : (int64_t)rr * a.y_stride + c));
+#pragma unroll
+    for (int j = 0; j < kUPT; ++j) {
+      const int u = tid + j * kNW * 64;
+      if (u < kUnits) {
+        const int rr = min(u / kRowUnits, a.m - 1);
+        const int c = n0 + 4 * (u % kRowUnits);
+        resid[j] = *reinterpret_cast<const u32x2 *>(a.y + (a.y_tiled ? tiled_index(rr, c, a.n) : (int64_t)rr * a.y_stride + c));
+      }
     }
   }
 
@@ -216,7 +229,7 @@ skinny_gemm_kernel(GemmArgs a) {
       for (int mt = 0; mt < MT; ++mt) {
         float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < kSsqVec; ++i) ss += (sv[mt][i][0] + sv[mt][i][1]) + (sv[mt][i][2] + sv[mt][i][3]);
+        for (int i = 0; i < kSsqV; ++i) ss += (sv[mt][i][0] + sv[mt][i][1]) + (sv[mt][i][2] + sv[mt][i][3]);
         ss += swizzle_xor16(ss);
         ss = sum_xor32(ss);
         rstd[mt] = rsqrtf(ss / (float)a.k + a.eps);
@@ -263,7 +276,7 @@ skinny_gemm_kernel(GemmArgs a) {
     for (int u = tid; u < NACC * TF / 4; u += kNW * 64) {
       const int t = u / (TF / 4);
       const int e = 4 * (u % (TF / 4));
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum_waves<kNW, NACC>(s_c, t, e)), prsrc,
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum_waves<kNW, NACC, TF>(s_c, t, e)), prsrc,
                                              ((slice * NACC + t) * TF + e) * (int)sizeof(float), 0, kCachePolicyAgent);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keep the stores above the wait
@@ -278,8 +291,9 @@ skinny_gemm_kernel(GemmArgs a) {
   }
 
   // Work unit u: 4 consecutive columns of one output row; the 8 units of 32 columns of a
-  // row sit in 8 consecutive lanes.
-  for (int u = tid; u < 32 * kRowUnits; u += kNW * 64) {
+  // row sit in 8 consecutive lanes.  j counts this thread's units.
+  int j = 0;
+  for (int u = tid; u < kUnits; u += kNW * 64, ++j) {
     const int row = u / kRowUnits;
     const int cl = 4 * (u % kRowUnits);  // column inside the workgroup's CW
     const int t = cl >> 4;
@@ -307,7 +321,7 @@ skinny_gemm_kernel(GemmArgs a) {
             if (s0 + q < a.ks) v[h] += ld[q];
         }
       } else {
-        v[h] = sum_waves<kNW, NACC>(s_c, tt, e);
+        v[h] = sum_waves<kNW, NACC, TF>(s_c, tt, e);
       }
     }
     const int c = n0 + cl;
@@ -321,7 +335,10 @@ skinny_gemm_kernel(GemmArgs a) {
       for (int q = 0; q < 4; ++q) o[q] = round_bf16(silu_f32(round_bf16(v[0][q]))) * round_bf16(v[NV - 1][q]);
       if (row < a.m) *reinterpret_cast<u32x2 *>(yp) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     } else {  // RESID
-      const u32x2 r = resid;  // unit u == tid
+      u32x2 r = resid[0];
+#pragma unroll
+      for (int q = 1; q < kUPT; ++q)
+        if (j == q) r = resid[q];
       const u32 h0 = pack_bf16x2(bf16_lo(r[0]) + round_bf16(v[0][0]), bf16_hi(r[0]) + round_bf16(v[0][1]));
       const u32 h1 = pack_bf16x2(bf16_lo(r[1]) + round_bf16(v[0][2]), bf16_hi(r[1]) + round_bf16(v[0][3]));
       float ss = bf16_lo(h0) * bf16_lo(h0) + bf16_hi(h0) * bf16_hi(h0) + bf16_lo(h1) * bf16_lo(h1) +
@@ -350,10 +367,12 @@ struct Plan {
 //     unsplit 16-wave workgroups: 8.2 us, faster only while the weights sit in the
 //     Infinity Cache);
 //   * otherwise (qkv, gate_up): 16 columns per 8-wave workgroup, no split.
-Plan make_plan(int n, int k, int epi) {
+// 64-row slabs (wide): the vocabulary-sized projection takes 64 columns per workgroup (128
+// would need 128 accumulator registers at 4 M tiles).
+Plan make_plan(int n, int k, int epi, bool wide) {
   Plan p{8, 1, 1, k % 512 == 0 ? 2 : 1};
   if (epi == kEpiStore && n % 128 == 0 && n / 128 >= 512) {
-    p = Plan{4, 8, 1, 2};
+    p = wide ? Plan{4, 4, 1, 2} : Plan{4, 8, 1, 2};
   } else if (epi == kEpiResid) {
     p = Plan{8, 2, 1, 2};
     const int groups = n / 32;
@@ -376,9 +395,29 @@ size_t workspace_bytes_for(const Plan &p, int n, int epi) {
   return kCounterBytes + kMaxSlabs * groups * p.ks * nacc * 32 * 16 * sizeof(float);
 }
 
+// Above 32 rows, 64-row slabs (wide) where the NORM prologue allows them (and not for a normed
+// residual projection, whose registers would spill); 32-row slabs otherwise.
+bool wide_rows(int m, int k, bool norm, int epi) {
+  return m > 32 && (!norm || (k <= kMaxWideNormK && epi != kEpiResid));
+}
+// Configurations 64-row slabs are built for (at most 64 columns per workgroup).
+template <int NT, int EPI, bool NORM>
+constexpr bool kWideBuilt = NT <= 4 && !(NORM && EPI == kEpiResid);
+
 template <int NW, int KB, int NT, int EPI, bool NORM>
-int launch(const GemmArgs &a, int grid, hipStream_t stream) {
-  if (a.m > 32)
+int launch(const GemmArgs &a, int grid, bool wide, hipStream_t stream) {
+  if (wide) {
+    if constexpr (kWideBuilt<NT, EPI, NORM>) {
+      if (a.m <= 64)
+        hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 4, EPI, NORM, false>), dim3(grid), dim3(NW * 64), 0,
+                           stream, a);
+      else
+        hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 4, EPI, NORM, true>), dim3(grid), dim3(NW * 64), 0,
+                           stream, a);
+    } else {
+      return NVAMD_EUNSUPPORTED;
+    }
+  } else if (a.m > 32)
     hipLaunchKernelGGL((skinny_gemm_kernel<NW, KB, NT, 2, EPI, NORM, true>), dim3(grid), dim3(NW * 64), 0, stream,
                        a);
   else if (a.m > 16)
@@ -391,19 +430,21 @@ int launch(const GemmArgs &a, int grid, hipStream_t stream) {
 }
 
 template <int NW, int NT, int EPI, bool NORM>
-int launch_kb(const GemmArgs &a, const Plan &p, int grid, hipStream_t stream) {
-  return p.kb == 2 ? launch<NW, 2, NT, EPI, NORM>(a, grid, stream) : launch<NW, 1, NT, EPI, NORM>(a, grid, stream);
+int launch_kb(const GemmArgs &a, const Plan &p, int grid, bool wide, hipStream_t stream) {
+  return p.kb == 2 ? launch<NW, 2, NT, EPI, NORM>(a, grid, wide, stream)
+                   : launch<NW, 1, NT, EPI, NORM>(a, grid, wide, stream);
 }
 
 template <int EPI, bool NORM>
-int dispatch(const GemmArgs &a, const Plan &p, int grid, hipStream_t stream) {
+int dispatch(const GemmArgs &a, const Plan &p, int grid, bool wide, hipStream_t stream) {
   if constexpr (EPI == kEpiStore) {
-    if (p.nw == 4 && p.nt == 8) return launch_kb<4, 8, EPI, NORM>(a, p, grid, stream);
+    if (p.nw == 4 && p.nt == 8) return launch_kb<4, 8, EPI, NORM>(a, p, grid, wide, stream);
+    if (p.nw == 4 && p.nt == 4) return launch_kb<4, 4, EPI, NORM>(a, p, grid, wide, stream);
   }
   if constexpr (EPI == kEpiResid) {
-    if (p.nw == 8 && p.nt == 2) return launch_kb<8, 2, EPI, NORM>(a, p, grid, stream);
+    if (p.nw == 8 && p.nt == 2) return launch_kb<8, 2, EPI, NORM>(a, p, grid, wide, stream);
   } else {
-    if (p.nw == 8 && p.nt == 1) return launch_kb<8, 1, EPI, NORM>(a, p, grid, stream);
+    if (p.nw == 8 && p.nt == 1) return launch_kb<8, 1, EPI, NORM>(a, p, grid, wide, stream);
   }
   return NVAMD_EUNSUPPORTED;
 }
@@ -415,8 +456,10 @@ using namespace nvamd;
 
 extern "C" size_t nvamd_skinny_linear_workspace_size(int n, int k, int epilogue) {
   if (n <= 0 || k <= 0 || n % 32 || k % 256 || epilogue < 0 || epilogue > 2) return 0;
-  const Plan p = make_plan(n, k, epilogue);
-  return workspace_bytes_for(p, n, epilogue);
+  // the larger of the two plans' needs (the row count is not known here)
+  const size_t slabs = workspace_bytes_for(make_plan(n, k, epilogue, false), n, epilogue);
+  const size_t wide = workspace_bytes_for(make_plan(n, k, epilogue, true), n, epilogue);
+  return slabs > wide ? slabs : wide;
 }
 
 extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float *x_ssq, const void *norm_weight,
@@ -437,10 +480,11 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
       (!x_tiled && (x_stride % 8 || x_stride < k)) || (!y_tiled && (y_stride < n || y_stride % 4)) ||
       (norm && (!aligned16(x_ssq) || !aligned16(norm_weight))))
     return NVAMD_EINVAL;
-  const Plan p = make_plan(n, k, epilogue);
+  const bool wide = wide_rows(m, k, norm, epilogue);
+  const Plan p = make_plan(n, k, epilogue, wide);
   const int groups = n / (16 * p.nt);
   if ((k / p.ks) % (32 * p.kb) != 0) return NVAMD_EUNSUPPORTED;  // whole wave blocks per slice
-  const int slabs = (m + 31) / 32;
+  const int slabs = wide ? (m + 63) / 64 : (m + 31) / 32;
   if (p.ks > 1) {
     if (groups * slabs > kCounterSlots) return NVAMD_EUNSUPPORTED;
     if (!workspace || !aligned16(workspace) || workspace_bytes < workspace_bytes_for(p, n, epilogue))
@@ -468,10 +512,10 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
   const int grid = groups * p.ks * slabs;
   switch (epilogue) {
     case kEpiSilu:
-      return norm ? dispatch<kEpiSilu, true>(a, p, grid, stream) : dispatch<kEpiSilu, false>(a, p, grid, stream);
+      return norm ? dispatch<kEpiSilu, true>(a, p, grid, wide, stream) : dispatch<kEpiSilu, false>(a, p, grid, wide, stream);
     case kEpiResid:
-      return norm ? dispatch<kEpiResid, true>(a, p, grid, stream) : dispatch<kEpiResid, false>(a, p, grid, stream);
+      return norm ? dispatch<kEpiResid, true>(a, p, grid, wide, stream) : dispatch<kEpiResid, false>(a, p, grid, wide, stream);
     default:
-      return norm ? dispatch<kEpiStore, true>(a, p, grid, stream) : dispatch<kEpiStore, false>(a, p, grid, stream);
+      return norm ? dispatch<kEpiStore, true>(a, p, grid, wide, stream) : dispatch<kEpiStore, false>(a, p, grid, wide, stream);
   }
 }
