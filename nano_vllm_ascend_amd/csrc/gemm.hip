@@ -368,11 +368,16 @@ struct Plan {
 //     Infinity Cache);
 //   * otherwise (qkv, gate_up): 16 columns per 8-wave workgroup, no split.
 // 64-row slabs (wide): the vocabulary-sized projection takes 64 columns per workgroup (128
-// would need 128 accumulator registers at 4 M tiles).
-Plan make_plan(int n, int k, int epi, bool wide) {
+// would need 128 accumulator registers at 4 M tiles); with two slabs (M > 64) the other
+// projections take 32 columns per workgroup, halving the X reads per weight byte (a projection
+// chain at M = 100: 35.2-35.8 against 41.4-42.1 us per layer; at M = 64, one slab, the halved
+// workgroup count makes it slower).
+Plan make_plan(int n, int k, int epi, int m, bool wide) {
   Plan p{8, 1, 1, k % 512 == 0 ? 2 : 1};
   if (epi == kEpiStore && n % 128 == 0 && n / 128 >= 512) {
     p = wide ? Plan{4, 4, 1, 2} : Plan{4, 8, 1, 2};
+  } else if (wide && m > 64 && epi != kEpiResid) {
+    p.nt = 2;
   } else if (epi == kEpiResid) {
     p = Plan{8, 2, 1, 2};
     const int groups = n / 32;
@@ -445,6 +450,7 @@ int dispatch(const GemmArgs &a, const Plan &p, int grid, bool wide, hipStream_t 
     if (p.nw == 8 && p.nt == 2) return launch_kb<8, 2, EPI, NORM>(a, p, grid, wide, stream);
   } else {
     if (p.nw == 8 && p.nt == 1) return launch_kb<8, 1, EPI, NORM>(a, p, grid, wide, stream);
+    if (p.nw == 8 && p.nt == 2) return launch_kb<8, 2, EPI, NORM>(a, p, grid, wide, stream);
   }
   return NVAMD_EUNSUPPORTED;
 }
@@ -457,8 +463,8 @@ using namespace nvamd;
 extern "C" size_t nvamd_skinny_linear_workspace_size(int n, int k, int epilogue) {
   if (n <= 0 || k <= 0 || n % 32 || k % 256 || epilogue < 0 || epilogue > 2) return 0;
   // the larger of the two plans' needs (the row count is not known here)
-  const size_t slabs = workspace_bytes_for(make_plan(n, k, epilogue, false), n, epilogue);
-  const size_t wide = workspace_bytes_for(make_plan(n, k, epilogue, true), n, epilogue);
+  const size_t slabs = workspace_bytes_for(make_plan(n, k, epilogue, 32, false), n, epilogue);
+  const size_t wide = workspace_bytes_for(make_plan(n, k, epilogue, 128, true), n, epilogue);
   return slabs > wide ? slabs : wide;
 }
 
@@ -481,7 +487,7 @@ extern "C" int nvamd_skinny_linear(const void *x, int64_t x_stride, const float 
       (norm && (!aligned16(x_ssq) || !aligned16(norm_weight))))
     return NVAMD_EINVAL;
   const bool wide = wide_rows(m, k, norm, epilogue);
-  const Plan p = make_plan(n, k, epilogue, wide);
+  const Plan p = make_plan(n, k, epilogue, m, wide);
   const int groups = n / (16 * p.nt);
   if ((k / p.ks) % (32 * p.kb) != 0) return NVAMD_EUNSUPPORTED;  // whole wave blocks per slice
   const int slabs = wide ? (m + 63) / 64 : (m + 31) / 32;
