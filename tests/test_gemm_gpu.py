@@ -1,4 +1,4 @@
-"""Skinny-M projection kernels (decode batches, M <= 32) against fp32 torch references.
+"""Skinny-M projection kernels (decode batches, M <= 128) against fp32 torch references.
 
 The kernel accumulates in fp32 and rounds to bf16 once, so each output is within one bf16 ulp of
 the fp32 product of the same bf16 operands: half an ulp is at most 2^-8 of the value, and the
@@ -130,9 +130,11 @@ def _tile_ssq(x):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 13, 32, 100])
-@pytest.mark.parametrize("nk", [(4096, 1024), (151936, 1024)], ids=["qkv", "lm_head"])
+@pytest.mark.parametrize("m", [1, 13, 32, 48, 100])
+@pytest.mark.parametrize("nk", [(4096, 1024), (151936, 1024), (1024, 2048)], ids=["qkv", "lm_head", "k2048"])
 def test_norm_prologue_matches_add_rms_norm_then_linear(device, m, nk):
+    """Above 32 rows the kernel takes 64-row slabs for k <= 1024 (one slab at 48 rows, two at 100)
+    and 32-row slabs for a larger k (k2048)."""
     n, k = nk
     x, w = _operands(m, n, k, device, seed=31 + m)
     gen = torch.Generator(device=device).manual_seed(5)
