@@ -181,7 +181,7 @@ skinny_gemm_kernel(GemmArgs a) {
     }
   }
 
-  // RESID: the residual values this thread adds in the epilogue (work unit u = tid, see there),
+  // RESID: the residual values this thread adds in the epilogue (work units u = tid + j * threads),
   // read now so that their load overlaps the weight stream instead of following the merge.  Only
   // this column group's merging workgroup writes them, after every read of this launch.
   constexpr int kRowUnits = CW / 4;
@@ -397,6 +397,7 @@ size_t workspace_bytes_for(const Plan &p, int n, int epi) {
   if (p.ks <= 1) return 0;
   const int nacc = (epi == kEpiSilu ? 2 : 1) * p.nt;
   const size_t groups = (size_t)n / (16 * p.nt);
+  // partial tiles for 128 rows: four 32-row slabs or two 64-row ones
   return kCounterBytes + kMaxSlabs * groups * p.ks * nacc * 32 * 16 * sizeof(float);
 }
 
