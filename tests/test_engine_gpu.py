@@ -184,7 +184,7 @@ def test_full_depth_greedy_tokens_against_oracle(device):
 @pytest.mark.parametrize("n_prompts", [4, 100])
 def test_fused_decode_path_matches_unfused_chain(device, n_prompts):
     """Decode batches <= 128 rows fold every RMSNorm and residual add into the projections (at
-    100 rows: four 32-row slabs per projection); the logits must match the unfused chain
+    100 rows: two 64-row slabs per projection); the logits must match the unfused chain
     (library GEMMs + add_rms_norm) of the same model to rounding, and tokens may differ only at
     near-ties."""
     kw = dict(graph=False) if n_prompts <= 8 else dict(graph=False, max_num_seqs=n_prompts, num_blocks=n_prompts * 3)
