@@ -320,3 +320,45 @@ def test_embed_rows_tiled(device, rows):
     got = _C.untile(out)
     assert torch.equal(got[:rows], ref) and torch.equal(ssq_t, ssq_rm)
     assert bool((got[rows:] == 7.0).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(6))
+def test_random_rows_and_epilogues(device, seed):
+    """Seeded random row counts around the slab boundaries (16, 32, 64, 65, 112, 128 rows), each
+    epilogue, with and without the norm prologue: every row equals the same projection of that row
+    alone (rows are independent; a one-row call takes the smallest configuration), bit for bit."""
+    import random
+    rng = random.Random(1000 + seed)
+    shapes = {_C.EPI_STORE: [(4096, 1024), (1024, 2048)], _C.EPI_SILU: [(3072, 1024)],
+              _C.EPI_RESID: [(1024, 2048), (1024, 3072)]}
+    for _ in range(3):
+        epi = rng.choice(list(shapes))
+        n, k = rng.choice(shapes[epi])
+        m = rng.choice([rng.randint(1, 128), rng.choice([16, 17, 32, 33, 63, 64, 65, 96, 112, 113, 127, 128])])
+        norm = epi != _C.EPI_RESID and rng.random() < 0.5
+        wrows = 2 * n if epi == _C.EPI_SILU else n
+        x, w = _operands(m, wrows, k, device, seed=seed * 101 + m)
+        wt = _C.tile(w)
+        gen = torch.Generator(device=device).manual_seed(seed)
+        nw = (1.0 + 0.02 * torch.randn(k, generator=gen, device=device)).to(torch.bfloat16) if norm else None
+        ssq = _tile_ssq(x).contiguous() if norm else None
+        ws = torch.zeros(max(_C.skinny_linear_workspace_size(n, k, epi), 16), dtype=torch.uint8, device=device)
+        if epi == _C.EPI_RESID:
+            r0 = torch.randn((m, n), generator=gen, device=device).to(torch.bfloat16)
+            y = r0.clone()
+            _C.skinny_linear(x, wt, y, epilogue=epi, y_ssq=torch.zeros((m, n // 32), device=device), workspace=ws)
+        else:
+            y = _C.skinny_linear(x, wt, epilogue=epi, x_ssq=ssq, norm_weight=nw, workspace=ws)
+        for row in sorted({0, m // 2, m - 1}):
+            sl = slice(row, row + 1)
+            if epi == _C.EPI_RESID:
+                y1 = r0[sl].clone()
+                _C.skinny_linear(x[sl], wt, y1, epilogue=epi, y_ssq=torch.zeros((1, n // 32), device=device),
+                                 workspace=ws)
+            else:
+                y1 = _C.skinny_linear(x[sl], wt, epilogue=epi, x_ssq=None if ssq is None else ssq[sl].contiguous(),
+                                      norm_weight=nw, workspace=ws)
+            torch.cuda.synchronize()
+            assert torch.equal(y[sl], y1), (f"epilogue {epi} norm {norm} m {m} n {n} k {k} row {row}: "
+                                            f"max diff {(y[sl].float() - y1.float()).abs().max().item():.3g}")
