@@ -65,6 +65,17 @@ def test_decode_long_contexts_many_partitions(device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("lo,hi,seed", [(16400, 32000, 23), (33000, 40960, 29)])
+def test_decode_very_long_contexts_several_chunks_per_wave(device, lo, hi, seed):
+    """Bounds past 64 partitions of 256 tokens (16,384 tokens) give each wave two 64-token chunks,
+    bounds past 32,768 tokens four; the second case reaches Qwen3's 40,960 positions."""
+    work = W.make_decode(2, lo, hi, 2 * (hi // 128 + 1), seed=seed, device=device)
+    assert max(work.context_lens_list) > 16384
+    check(work)
+    check(work, max_ctx=40960)  # the four-chunk launch over shorter contexts
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("case", ["ramp", "large"])
 def test_decode_partitions_with_far_apart_maxima(device, case):
     """Keys scaled up along each context (ramp: later partitions' maxima exceed earlier ones by tens
