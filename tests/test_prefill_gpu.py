@@ -97,6 +97,27 @@ def test_dense_prefill_32_ragged_prompts(device):
     assert err <= TOL, err
 
 
+@pytest.mark.gpu
+def test_dense_prefill_long_prompts(device):
+    """Prompts of 12,000 and 20,000 tokens (up to 625 key tiles per query tile).  The oracle
+    attends a spread of rows of each prompt, its first and last tiles included, over their full
+    causal prefix."""
+    from oracle.attention_ref import _attend
+
+    lens = [12000, 20000]
+    out, q, k, v, cu = run_dense(lens, 16, 8, device, seed=21)
+    out, q, k, v = out.float().cpu(), q.cpu(), k.cpu(), v.cpu()
+    gen = torch.Generator().manual_seed(21)
+    for s, n in enumerate(lens):
+        a = cu[s]
+        picked = torch.randint(0, n, (24,), generator=gen).tolist()
+        rows = torch.tensor(sorted({0, 1, 31, 32, 63, 64, 127, 128, n // 2, n - 129, n - 64, n - 1, *picked}))
+        allowed = torch.arange(n)[None, :] <= rows[:, None]
+        ref = _attend(q[a + rows], k[a : a + n], v[a : a + n], SCALE, allowed)
+        err = (out[a + rows] - ref).abs().max().item()
+        assert err <= TOL, (n, err)
+
+
 def _paged_case(device, prompt_lens, cached, bs=128, seed=0, hq=16, hkv=8, qkv=None):
     """Full prompts written to a paged cache; queries = the suffix after `cached` tokens.  `qkv`
     gives the prompts' (q, k, v) instead of seeded N(0, 1) ones."""
