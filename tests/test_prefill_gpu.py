@@ -172,6 +172,21 @@ def test_paged_prefix_hit_prefill(device, bs):
 
 
 @pytest.mark.gpu
+def test_paged_prefill_long_cached_prefixes(device):
+    """Prefix hits of 17,500 and 8,800 cached tokens (137 and 69 pages) ahead of 500 and 200 new
+    query rows: against the oracle, and equal to the dense prefill rows of the whole prompts."""
+    prompt_lens, cached = [18000, 9000], [17500, 8800]
+    out, qs, q, k, v, kc, vc, tables, cu_q, cu_full, sel = _paged_case(device, prompt_lens, cached, seed=31)
+    ref = paged_prefill_ref(qs, kc, vc, tables, cu_q, prompt_lens, SCALE)
+    assert (out.float().cpu() - ref).abs().max().item() <= TOL
+    dense = torch.empty(q.shape, dtype=torch.bfloat16, device=device)
+    _C.varlen_prefill(dense, q, k, v, torch.tensor(cu_full, dtype=torch.int32, device=device), max(prompt_lens),
+                      SCALE)
+    torch.cuda.synchronize()
+    assert (out.float() - dense[sel].float()).abs().max().item() <= TOL
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("heads", [(40, 8), (32, 4)])
 def test_paged_prefill_gqa_launch_groups(device, heads):
     """Ratios 5 and 8 run as several launches over 4, 2 and 1 query heads of every kv head."""
