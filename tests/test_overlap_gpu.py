@@ -56,3 +56,34 @@ def test_overlapped_engine_metadata_equals_oracle_replay(device):
     assert_same_metadata(events, ref)
     del llm
     torch.cuda.empty_cache()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed,bs,blocks,seqs,prefix", [(41, 128, 60, 8, True), (42, 64, 90, 6, False),
+                                                        (43, 16, 400, 8, True)])
+def test_random_schedules_metadata_equals_oracle_replay(device, seed, bs, blocks, seqs, prefix):
+    """Seeded schedules of 12 requests (prompts of 20-300 tokens behind a shared 2-block prefix on
+    even requests when the cache is on, 5-120 new tokens, half admitted mid-run), block sizes 128,
+    64 and 16, up to 8 running sequences (decode graphs of 1-8 rows), overlapped decode, an EOS the
+    model samples mid-run: every prefill and decode step's metadata equals the oracle engine's
+    replay of the same run."""
+    schedule = make_schedule(seed=seed, n=12, block_size=bs, len_lo=20, len_hi=300, new_lo=5, new_hi=120,
+                             shared_blocks=2 if prefix else 0)
+
+    def build():
+        return LLM(SMALL, max_model_len=1024, block_size=bs, num_blocks=blocks, max_num_seqs=seqs,
+                   enable_prefix_cache=prefix, enable_decode_graph=True, seed=seed, enable_overlap=True)
+
+    _, plain, _ = run_product(build(), schedule, -1)
+    longest = max(plain, key=lambda i: len(plain[i]))
+    eos = plain[longest][len(plain[longest]) // 2]
+    llm = build()
+    events, out, reasons = run_product(llm, schedule, eos)
+    print(f"[random schedule {seed}] bs {bs}: {len(events)} steps, overlap {dict(llm.runner.overlap_stats)}, "
+          f"finish reasons {sorted(set(reasons.values()))}", flush=True)
+    assert "eos" in reasons.values()
+    ref = oracle_replay(schedule, out, reasons, eos, block_size=bs, num_blocks=blocks, max_num_seqs=seqs,
+                        prefix=prefix)
+    assert_same_metadata(events, ref)
+    del llm
+    torch.cuda.empty_cache()
