@@ -69,6 +69,34 @@ def test_ragged_prefill_packing_32_prompts(device):
 
 
 @pytest.mark.gpu
+def test_packing_at_scale_small_blocks(device):
+    """256 prompts of U[1, 4096] tokens in 16-token blocks (tables up to 256 entries wide) from a
+    seeded free list, then 20 decode steps at batch 256: every step's slot mapping, tables and
+    context lengths equal the oracle block manager's."""
+    rng = random.Random(5)
+    lens = [rng.randint(1, 4096) for _ in range(256)]
+    num_blocks = sum((n + 20 + 15) // 16 for n in lens) + 64
+    ref, bm = _seeded_pair(num_blocks, 16, seed=5, device=device, max_seqs=256)
+    slots = list(range(256))
+
+    def same(a, b, step):
+        torch.cuda.synchronize()
+        w = a.block_tables.shape[1]
+        got = b.block_tables.cpu()
+        assert torch.equal(got[:, :w], a.block_tables), step
+        assert not got[:, w:].any(), step
+        assert torch.equal(b.slot_mapping.cpu(), a.slot_mapping), step
+        assert torch.equal(b.context_lens.cpu(), a.context_lens), step
+
+    same(ref.prepare_prefill_metadata(slots, lens, [0] * 256, [[] for _ in slots]),
+         bm.prepare_prefill_metadata(slots, lens, [0] * 256, [[] for _ in slots]), "prefill")
+    pos = list(lens)
+    for step in range(20):
+        same(ref.prepare_decode_metadata(slots, pos, 1), bm.prepare_decode_metadata(slots, pos, 1), step)
+        pos = [p + 1 for p in pos]
+
+
+@pytest.mark.gpu
 def test_decode_packing_into_static_graph_buffers(device):
     """Decode steps packed into fixed-width buffers; new blocks appear at page boundaries."""
     ref, bm = _seeded_pair(256, 16, seed=3, device=device, max_seqs=2, max_blocks_per_seq=2)
