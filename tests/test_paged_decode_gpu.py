@@ -76,6 +76,18 @@ def test_decode_very_long_contexts_several_chunks_per_wave(device, lo, hi, seed)
 
 
 @pytest.mark.gpu
+def test_decode_at_the_two_chunk_boundary(device):
+    """Bounds of 16,384 and 16,385 tokens take one and two chunks per wave; contexts at and around
+    the boundary, and short ones, give the same results under both."""
+    work = W.make_decode(4, 0, 0, 4 * 129, seed=37, device=device, context_lens=[16384, 16383, 16385, 300])
+    a = check(work, max_ctx=16385)
+    short = W.make_decode(3, 0, 0, 3 * 129, seed=38, device=device, context_lens=[16384, 1, 7000])
+    check(short, max_ctx=16384)
+    check(short, max_ctx=16385)
+    assert a <= TOL
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("case", ["ramp", "large"])
 def test_decode_partitions_with_far_apart_maxima(device, case):
     """Keys scaled up along each context (ramp: later partitions' maxima exceed earlier ones by tens
